@@ -1,0 +1,64 @@
+"""ctypes binding of the C-ABI kernel library (include/gss.h). Loading fails loudly when the library is missing:
+there is no CPU or eager fallback on the product path."""
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libgss.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "gss.h")
+
+_p, _i, _i64, _sz, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_float
+_psz = ctypes.POINTER(ctypes.c_size_t)
+
+# argument types of every entry point, in header order
+SIGNATURES = {
+    "gss_version": ([], ctypes.c_char_p),
+    "gss_status_string": ([_i], ctypes.c_char_p),
+    "gss_attn_workspace_size": ([_i, _i, _i, _i, _i, _i, _psz], _i),
+    "gss_draft_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
+    "gss_verify_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
+    "gss_argmax_workspace_size": ([_i, _i, _i, _psz], _i),
+    "gss_argmax_accept": ([_p, _i, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
+    "gss_kv_commit_workspace_size": ([_i, _psz], _i),
+    "gss_kv_commit": ([_p, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
+    "gss_rope_stage": ([_p, _i64, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "gss_rmsnorm": ([_p, _p, _p, _i, _i, _f, _p], _i),
+    "gss_add_rmsnorm": ([_p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
+    "gss_silu_mul": ([_p, _i64, _p, _i, _i, _p], _i),
+}
+
+_LIB = None
+
+
+class GssError(RuntimeError):
+    pass
+
+
+def header_symbols():
+    """Function names declared in include/gss.h."""
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(gss_\w+)\s*\(", txt, flags=re.M)
+
+
+def lib():
+    """Load libgss.so once and declare the prototypes. Raises if the library has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise GssError(f"{LIB_PATH} is missing: build it with `python -m gravityocr_amd.build` "
+                           "(the HIP kernels have no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (args, res) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = res
+        _LIB = L
+    return _LIB
+
+
+def check(status: int, what: str):
+    if status != 0:
+        msg = lib().gss_status_string(status).decode()
+        raise GssError(f"{what}: {msg} (status {status})")

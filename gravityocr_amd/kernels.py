@@ -1,0 +1,157 @@
+"""torch-tensor front end of the C-ABI kernels. Every function validates shapes / dtypes / devices on the host
+(the kernels trust their arguments), launches on torch's current stream and raises on a non-zero status."""
+import ctypes
+from typing import Optional
+
+import torch
+
+from ._lib import check, lib
+
+PAGE = 16
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _need(t: torch.Tensor, dtype, name: str, shape=None):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+def attn_workspace_bytes(bs, Hq, Hkv, D, W, max_kv_len) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().gss_attn_workspace_size(bs, Hq, Hkv, D, W, max_kv_len, ctypes.byref(n)), "gss_attn_workspace_size")
+    return n.value
+
+
+def argmax_workspace_bytes(bs, W, V) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().gss_argmax_workspace_size(bs, W, V, ctypes.byref(n)), "gss_argmax_workspace_size")
+    return n.value
+
+
+def commit_workspace_bytes(bs) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().gss_kv_commit_workspace_size(bs, ctypes.byref(n)), "gss_kv_commit_workspace_size")
+    return n.value
+
+
+def window_attention(q, k_pages, v_pages, page_table, prefix_len, k_win, v_win, out, *, n_causal: Optional[int],
+                     scale: float, max_kv_len: int, workspace: Optional[torch.Tensor], prefix_extra: int = 0):
+    """Draft (n_causal given) or verify (n_causal None) attention. Shapes: q/out [bs, W, Hq, D] bf16,
+    k_pages [n_pages, Hkv, 16, D], v_pages [n_pages, Hkv, D, 16], page_table int32 [bs, P], prefix_len int32 [bs],
+    k_win/v_win [bs, W, Hkv, D]."""
+    bs, W, Hq, D = q.shape
+    n_pages, Hkv = k_pages.shape[0], k_pages.shape[1]
+    _need(q, torch.bfloat16, "q")
+    _need(out, torch.bfloat16, "out", q.shape)
+    _need(k_pages, torch.bfloat16, "k_pages", (n_pages, Hkv, PAGE, D))
+    _need(v_pages, torch.bfloat16, "v_pages", (n_pages, Hkv, D, PAGE))
+    _need(k_win, torch.bfloat16, "k_win", (bs, W, Hkv, D))
+    _need(v_win, torch.bfloat16, "v_win", (bs, W, Hkv, D))
+    _need(page_table, torch.int32, "page_table")
+    _need(prefix_len, torch.int32, "prefix_len", (bs,))
+    if page_table.shape[0] != bs:
+        raise ValueError("page_table rows != batch")
+    if max_kv_len > page_table.shape[1] * PAGE:
+        raise ValueError("max_kv_len exceeds what the page table addresses")
+    need = attn_workspace_bytes(bs, Hq, Hkv, D, W, max_kv_len)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if need > ws_bytes:
+        raise ValueError(f"attention workspace {ws_bytes} B < {need} B")
+    L = lib()
+    common = (_ptr(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table), page_table.shape[1], _ptr(prefix_len),
+              prefix_extra, _ptr(k_win), _ptr(v_win), _ptr(out), bs, W)
+    tail = (Hq, Hkv, D, PAGE, float(scale), int(max_kv_len), _ptr(workspace), ws_bytes, _stream())
+    if n_causal is None:
+        check(L.gss_verify_attn(*common, *tail), "gss_verify_attn")
+    else:
+        check(L.gss_draft_attn(*common, int(n_causal), *tail), "gss_draft_attn")
+    return out
+
+
+def argmax_accept(logits, target, workspace, *, window=None, accept_len=None, next_x0=None, packed=None):
+    """logits [bs, W, V] (bf16 or fp32, rows may be strided: logits.stride(1) is the row stride, last dim dense);
+    target int32 [bs, W]. With ``window`` (int32 [bs, W]) also accept_len / next_x0 [bs] and packed [bs, W+2]."""
+    bs, W, V = logits.shape
+    if not logits.is_cuda or logits.stride(2) != 1 or logits.stride(0) != W * logits.stride(1):
+        raise ValueError("logits must be a GPU tensor [bs, W, V] with dense rows and a uniform row stride")
+    dt = {torch.bfloat16: 0, torch.float32: 1}.get(logits.dtype)
+    if dt is None:
+        raise ValueError("logits must be bf16 or fp32")
+    _need(target, torch.int32, "target", (bs, W))
+    for name, t, shp in (("window", window, (bs, W)), ("accept_len", accept_len, (bs,)),
+                         ("next_x0", next_x0, (bs,)), ("packed", packed, (bs, W + 2))):
+        if t is not None:
+            _need(t, torch.int32, name, shp)
+    need = argmax_workspace_bytes(bs, W, V)
+    if workspace.numel() * workspace.element_size() < need:
+        raise ValueError("argmax workspace too small")
+    check(lib().gss_argmax_accept(_ptr(logits), dt, logits.stride(1), bs, W, V, _ptr(window), _ptr(target),
+                                  _ptr(accept_len), _ptr(next_x0), _ptr(packed), _ptr(workspace),
+                                  workspace.numel() * workspace.element_size(), _stream()), "gss_argmax_accept")
+
+
+def kv_commit(k_win, v_win, k_pages, v_pages, page_table, seq_lens, workspace, *, n_rows=None, n_add=0,
+              slots=None):
+    """k_win/v_win [n_layers, bs, W, Hkv, D]; k_pages [n_layers, n_pages, Hkv, 16, D]; v_pages
+    [n_layers, n_pages, Hkv, D, 16]; seq_lens int32 [bs] (advanced in place); n_rows int32 [bs] or None;
+    slots int32 [bs, W] or None."""
+    nl, bs, W, Hkv, D = k_win.shape
+    _need(k_win, torch.bfloat16, "k_win")
+    _need(v_win, torch.bfloat16, "v_win", k_win.shape)
+    _need(k_pages, torch.bfloat16, "k_pages")
+    _need(v_pages, torch.bfloat16, "v_pages")
+    if k_pages.shape[0] != nl or k_pages.shape[2:] != (Hkv, PAGE, D) or v_pages.shape[2:] != (Hkv, D, PAGE):
+        raise ValueError("page tensors do not match the window tensors")
+    _need(page_table, torch.int32, "page_table")
+    _need(seq_lens, torch.int32, "seq_lens", (bs,))
+    if n_rows is not None:
+        _need(n_rows, torch.int32, "n_rows", (bs,))
+    if slots is not None:
+        _need(slots, torch.int32, "slots", (bs, W))
+    wsb = workspace.numel() * workspace.element_size()
+    check(lib().gss_kv_commit(_ptr(k_win), _ptr(v_win), bs * W * Hkv * D, _ptr(k_pages), _ptr(v_pages),
+                              k_pages[0].numel(), _ptr(page_table), page_table.shape[1], _ptr(seq_lens),
+                              _ptr(n_rows), int(n_add), _ptr(slots), bs, W, nl, Hkv, D, PAGE, _ptr(workspace), wsb,
+                              _stream()), "gss_kv_commit")
+
+
+def rope_stage(qkv, seq_lens, inv_freq, q, k_win, v_win, *, pos_offset=0, pos_delta=None, rot_dim: int):
+    """qkv [bs*W, (Hq+2Hkv)*D] bf16 (row stride qkv.stride(0)); q [bs, W, Hq, D]; k_win/v_win [bs, W, Hkv, D]."""
+    bs, W, Hq, D = q.shape
+    Hkv = k_win.shape[2]
+    if qkv.stride(1) != 1 or qkv.shape[0] != bs * W or qkv.shape[1] < (Hq + 2 * Hkv) * D:
+        raise ValueError("qkv shape")
+    _need(seq_lens, torch.int32, "seq_lens", (bs,))
+    _need(inv_freq, torch.float32, "inv_freq", (rot_dim // 2,))
+    check(lib().gss_rope_stage(_ptr(qkv), qkv.stride(0), _ptr(seq_lens), _ptr(pos_delta), int(pos_offset),
+                               _ptr(inv_freq), rot_dim, _ptr(q), _ptr(k_win), _ptr(v_win), bs, W, Hq, Hkv, D,
+                               _stream()), "gss_rope_stage")
+
+
+def rmsnorm(x, w, out, eps):
+    rows, H = x.shape
+    check(lib().gss_rmsnorm(_ptr(x), _ptr(w), _ptr(out), rows, H, float(eps), _stream()), "gss_rmsnorm")
+
+
+def add_rmsnorm(a, w_post, h, w_next, x, eps):
+    rows, H = h.shape
+    check(lib().gss_add_rmsnorm(_ptr(a), _ptr(w_post), _ptr(h), _ptr(w_next), _ptr(x), rows, H, float(eps),
+                                _stream()), "gss_add_rmsnorm")
+
+
+def silu_mul(gu, out):
+    rows, F = out.shape
+    check(lib().gss_silu_mul(_ptr(gu), gu.stride(0), _ptr(out), rows, F, _stream()), "gss_silu_mul")

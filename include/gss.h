@@ -1,0 +1,135 @@
+/*
+ * gss.h — C ABI of the MI355X (gfx950) self-speculative round kernels.
+ *
+ * Every entry point takes raw device pointers, explicit sizes and a HIP stream (passed as an opaque pointer, the
+ * value of hipStream_t), enqueues its kernels on that stream and returns a status code; nothing synchronises and
+ * nothing allocates. The caller owns every buffer. Lengths that change from round to round (committed KV length,
+ * accept length) are read from device memory, so a sequence of calls can be captured into a HIP graph and replayed.
+ *
+ * Tensor layouts (bf16 = 16-bit brain float, stored as its bit pattern):
+ *   q            [bs, W, Hq, D]                   window queries, already rotated
+ *   k_pages      [n_pages, Hkv, page, D]          paged K cache (one layer)
+ *   v_pages      [n_pages, Hkv, D, page]          paged V cache (one layer), token index fastest within a page
+ *   page_table   int32 [bs, pt_stride]            page ids of each sequence, in position order
+ *   k_win, v_win [bs, W, Hkv, D]                  the window's own K/V (staging, not yet in the cache)
+ *   logits       [bs, W, V] (row stride ld_row elements), bf16 or fp32
+ *
+ * Greedy rule shared with the reference: index of the row maximum, lowest index on exact ties, NaN counts as max.
+ */
+#ifndef GSS_H
+#define GSS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* gss_stream_t; /* a hipStream_t; NULL = the default stream */
+
+enum gss_status {
+  GSS_OK = 0,
+  GSS_ERR_ARG = 1,         /* a size, stride or pointer is invalid */
+  GSS_ERR_UNSUPPORTED = 2, /* a shape the kernels are not built for (head_dim, page size, window, group) */
+  GSS_ERR_WORKSPACE = 3,   /* workspace missing or smaller than the size query returned */
+  GSS_ERR_LAUNCH = 4       /* the HIP launch itself failed */
+};
+
+enum gss_dtype { GSS_BF16 = 0, GSS_F32 = 1 };
+
+const char* gss_version(void);
+const char* gss_status_string(int status);
+
+/* ---------------------------------------------------------------- (a)/(b) attention over paged KV + window ---
+ * Replaces the draft/verify attention of the self-spec forwards: the flashinfer paged prefill the SGLang hooks
+ * route by role (patches/sglang/sglang_0.5.10_selfspec.patch:486-522; planner
+ * patches/sglang/python/sglang/srt/speculative/selfspec_fast_attn.py:168-465) and the flex-attention masks of the
+ * in-process drop-in (src/fast_sampling.py:508-514).
+ *
+ * Query row w of sequence b attends to the committed prefix, keys [0, L) with L = prefix_len[b] + prefix_extra,
+ * read from the pages, and to window keys from k_win/v_win:
+ *   draft  (gss_draft_attn):  rows w < n_causal see window rows 0..w; rows w >= n_causal see all W window rows.
+ *                             n_causal = 1 is the serving draft [x0 | MASK x B] and natcache rounds >= 1;
+ *                             n_causal = 0 is natcache round 0 and the block-diffusion sampler's full block.
+ *   verify (gss_verify_attn): row w sees window rows 0..w (causal, bottom-right aligned).
+ * scale multiplies q.k (1/sqrt(D) for GLM). max_kv_len bounds L over the batch and sizes the split-KV grid;
+ * the workspace must hold gss_attn_workspace_size(...) bytes and must be zeroed once after allocation (the kernels
+ * leave it reusable). Supported: D in {64, 128}, page = 16, 1 <= W <= 64, Hq % Hkv == 0, Hq/Hkv * W <= 512.
+ */
+int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes);
+
+int gss_draft_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int pt_stride,
+                   const int32_t* prefix_len, int prefix_extra, const void* k_win, const void* v_win, void* out,
+                   int bs, int W, int n_causal, int Hq, int Hkv, int D, int page, float scale, int max_kv_len,
+                   void* workspace, size_t workspace_bytes, gss_stream_t stream);
+
+int gss_verify_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
+                    int pt_stride, const int32_t* prefix_len, int prefix_extra, const void* k_win, const void* v_win,
+                    void* out, int bs, int W, int Hq, int Hkv, int D, int page, float scale, int max_kv_len,
+                    void* workspace, size_t workspace_bytes, gss_stream_t stream);
+
+/* ---------------------------------------------------------------- (c) argmax + accept + bonus -------------------
+ * Replaces torch.argmax over the verify/draft logits (selfspec_diffusion_worker.py:742; src/fast_sampling.py:545,
+ * :574-575) and sgl-kernel verify_tree_greedy on the worker's linear chain (selfspec_fast_commit.py:150-160,
+ * chain layout selfspec_diffusion_worker.py:530-548).
+ *
+ * target[b, r] = argmax of logits row (b, r), r in [0, W).
+ * With window != NULL (the verify ids [a0, d_1..d_{W-1}] of each sequence) also:
+ *   accept_len[b] = number of leading r in [0, W-2] with target[b, r] == window[b, r+1]
+ *   next_x0[b]    = target[b, accept_len[b]]              (the correction, or the bonus when all W-1 matched)
+ *   packed[b]     = (window[b,0], accept_len[b], target[b,0..W-1] with entries past accept_len zeroed)
+ *                   the row layout of _ss_commit_kernel's readback (selfspec_fast_commit.py:125-138); may be NULL.
+ * Workspace: gss_argmax_workspace_size bytes, zeroed once after allocation.
+ */
+int gss_argmax_workspace_size(int bs, int W, int V, size_t* bytes);
+
+int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, int bs, int W, int V, const int32_t* window,
+                      int32_t* target, int32_t* accept_len, int32_t* next_x0, int32_t* packed, void* workspace,
+                      size_t workspace_bytes, gss_stream_t stream);
+
+/* ---------------------------------------------------------------- (d) KV commit ---------------------------------
+ * Replaces the commit half of _ss_commit_kernel (selfspec_fast_commit.py:139-147: seq_lens += acc + 1, rejected
+ * slots released) and the natcache cache truncation (src/fast_sampling.py:600-605): the first n_b rows of the
+ * window K/V of every layer are written into the pages at positions seq_lens[b] + j, j < n_b, and
+ * seq_lens[b] += n_b, with n_b = (n_rows ? n_rows[b] : 0) + n_add. Rows >= n_b are discarded in place (never
+ * written; the staging is overwritten by the next forward). slots (optional, [bs, W]) receives the slot index
+ * page_table[b][pos / page] * page + pos % page of each committed row, -1 for the rest.
+ * Window/page tensors of layer l start at k_win + l * win_layer_stride (elements), k_pages + l * page_layer_stride.
+ * Workspace: gss_kv_commit_workspace_size bytes (per-sequence counters), zeroed once after allocation.
+ */
+int gss_kv_commit_workspace_size(int bs, size_t* bytes);
+
+int gss_kv_commit(const void* k_win, const void* v_win, int64_t win_layer_stride, void* k_pages, void* v_pages,
+                  int64_t page_layer_stride, const int32_t* page_table, int pt_stride, int32_t* seq_lens,
+                  const int32_t* n_rows, int n_add, int32_t* slots, int bs, int W, int n_layers, int Hkv, int D,
+                  int page, void* workspace, size_t workspace_bytes, gss_stream_t stream);
+
+/* ---------------------------------------------------------------- decoder-layer helpers -------------------------
+ * Fused elementwise pieces of the GLM text decoder layer (transformers GlmOcrTextDecoderLayer, which the reference
+ * calls through src/fast_sampling.py:89-102). bf16 in and out; fp32 inside; every step rounds to bf16 where the
+ * reference's bf16 module does.
+ *
+ * gss_rope_stage: split the fused q|k|v projection rows, rotate q and k (interleaved pairs over the first rot_dim
+ * dims, position = seq_lens[b] + (pos_delta ? pos_delta[b] : 0) + pos_offset + w), write q [bs, W, Hq, D] and the
+ * window K/V [bs, W, Hkv, D].
+ */
+int gss_rope_stage(const void* qkv, int64_t ld_qkv, const int32_t* seq_lens, const int32_t* pos_delta,
+                   int pos_offset, const float* inv_freq, int rot_dim, void* q, void* k_win, void* v_win, int bs,
+                   int W, int Hq, int Hkv, int D, gss_stream_t stream);
+
+/* out = rmsnorm(x) * w  (GlmOcrRMSNorm), rows x H. */
+int gss_rmsnorm(const void* x, const void* w, void* out, int rows, int H, float eps, gss_stream_t stream);
+
+/* h = h + rmsnorm(a) * w_post;  x = rmsnorm(h) * w_next   (sandwich-norm residual, then the next norm). */
+int gss_add_rmsnorm(const void* a, const void* w_post, void* h, const void* w_next, void* x, int rows, int H,
+                    float eps, gss_stream_t stream);
+
+/* out[r, :F] = up * silu(gate) with gu[r] = [gate (F) | up (F)], row stride ld_gu elements (GlmOcrTextMLP). */
+int gss_silu_mul(const void* gu, int64_t ld_gu, void* out, int rows, int F, gss_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSS_H */

@@ -1,0 +1,102 @@
+"""Parity of the draft (a) / verify (b) attention kernels with the oracle's explicit-mask attention.
+
+Kernel-only workload: 1 sequence, 16 q / 2 kv heads, head_dim 128, committed prefix L in {1K, 4K, 8K, 16K} in
+16-token pages in a shuffled page order, 17 window rows (boundary token + 16 masks), Q/K/V ~ N(0,1)/sqrt(128),
+seed 1; draft mask (row 0 causal, rows 1.. bidirectional) and verify mask (causal). Tolerance: max |err| <=
+1e-2 * max |ref| (bf16 output). Unused cache slots hold NaN, so a read outside the committed prefix would show.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import masked_attention, window_mask
+from tests.helpers import ATTN_REL, PAGE, rel_err, shuffled_page_table
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, Ls, W, n_causal, Hq=16, Hkv=2, D=128, seed=1, max_kv_len=None, prefix_extra=0, verify=False):
+    bs = len(Ls)
+    g = torch.Generator().manual_seed(seed)
+    sc = D ** -0.5
+    Lmax = max(Ls) + prefix_extra
+    cap = max_kv_len if max_kv_len is not None else Lmax
+    ppseq = max(1, (cap + PAGE - 1) // PAGE)
+    n_pages = bs * ppseq + 3
+    pt = shuffled_page_table(bs, ppseq, n_pages, seed)
+    k_pages = torch.full((n_pages, Hkv, PAGE, D), float("nan"), dtype=torch.bfloat16)
+    v_pages = torch.full((n_pages, Hkv, D, PAGE), float("nan"), dtype=torch.bfloat16)
+    q = (torch.randn(bs, W, Hq, D, generator=g) * sc).bfloat16()
+    k_win = (torch.randn(bs, W, Hkv, D, generator=g) * sc).bfloat16()
+    v_win = (torch.randn(bs, W, Hkv, D, generator=g) * sc).bfloat16()
+    refs = []
+    for b, L0 in enumerate(Ls):
+        L = L0 + prefix_extra
+        k = (torch.randn(L, Hkv, D, generator=g) * sc).bfloat16()
+        v = (torch.randn(L, Hkv, D, generator=g) * sc).bfloat16()
+        if L:
+            pos = torch.arange(L)
+            pg = torch.as_tensor(pt[b])[pos // PAGE].long()
+            k_pages[pg, :, pos % PAGE, :] = k
+            v_pages[pg, :, :, pos % PAGE] = v
+        nc = W if verify else n_causal
+        refs.append(masked_attention(q[b], torch.cat([k, k_win[b]]), torch.cat([v, v_win[b]]),
+                                     window_mask(L, W, nc), sc))
+    from gravityocr_amd.kernels import attn_workspace_bytes, window_attention
+    ws = torch.zeros(max(1, attn_workspace_bytes(bs, Hq, Hkv, D, W, cap)), dtype=torch.uint8, device=dev)
+    out = torch.empty(bs, W, Hq, D, dtype=torch.bfloat16, device=dev)
+    window_attention(q.to(dev), k_pages.to(dev), v_pages.to(dev), torch.as_tensor(pt).to(dev),
+                     torch.tensor(Ls, dtype=torch.int32, device=dev), k_win.to(dev), v_win.to(dev), out,
+                     n_causal=None if verify else n_causal, scale=sc, max_kv_len=cap, workspace=ws,
+                     prefix_extra=prefix_extra)
+    torch.cuda.synchronize()
+    out = out.cpu()
+    assert torch.isfinite(out.float()).all()
+    for b in range(bs):
+        e = rel_err(out[b], refs[b])
+        assert e <= ATTN_REL, (b, Ls[b], e)
+    return out, refs
+
+
+@pytest.mark.parametrize("L", [1024, 4096, 8192, 16384])
+@pytest.mark.parametrize("verify", [False, True])
+def test_block_attention_config(cuda, L, verify):
+    print(f"attn L={L} verify={verify}", flush=True)
+    run_case(cuda, [L], 17, 1, verify=verify)
+
+
+@pytest.mark.parametrize("L", [0, 1, 15, 16, 17, 63, 64, 65, 130, 1000])
+@pytest.mark.parametrize("n_causal", [0, 1, 17])
+def test_draft_mask_edges(cuda, L, n_causal):
+    print(f"edge L={L} nc={n_causal}", flush=True)
+    run_case(cuda, [L], 17, n_causal, seed=L + 7)
+
+
+@pytest.mark.parametrize("W", [1, 2, 5, 9, 33, 34])
+def test_window_sizes(cuda, W):
+    print(f"W={W}", flush=True)
+    run_case(cuda, [777], W, 1, seed=W)
+    run_case(cuda, [777], W, 1, seed=W, verify=True)
+
+
+def test_ragged_batch_and_capacity(cuda):
+    # ragged prefixes, a capacity (max_kv_len) far above the actual lengths, as a captured graph would use
+    run_case(cuda, [1024, 3, 4097, 0, 12288], 17, 1, max_kv_len=16384, seed=3)
+    run_case(cuda, [1024, 3, 4097, 0, 12288], 9, 1, max_kv_len=16384, seed=4, verify=True)
+
+
+def test_prefix_extra(cuda):
+    # verify after an in-round x0 commit: prefix = seq_len + 1
+    run_case(cuda, [500, 2047], 17, 1, prefix_extra=1, verify=True, seed=5)
+
+
+def test_tiny_head_dim_64(cuda):
+    # the CPU plumbing decoder's shape: 4 q / 2 kv heads, head_dim 64
+    run_case(cuda, [272], 5, 1, Hq=4, Hkv=2, D=64, seed=6)
+    run_case(cuda, [272, 31], 6, 6, Hq=4, Hkv=2, D=64, seed=7, verify=True)
+
+
+def test_deterministic(cuda):
+    a, _ = run_case(cuda, [8192], 17, 1, seed=11)
+    b, _ = run_case(cuda, [8192], 17, 1, seed=11)
+    assert torch.equal(a, b)
