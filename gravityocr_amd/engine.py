@@ -1,0 +1,256 @@
+"""The self-speculative round on one MI355X: GLM decoder forward over a paged KV cache through the C-ABI kernels,
+with every round-to-round quantity (committed lengths, boundary tokens, accept lengths) resident on the device so a
+whole round is captured once as a HIP graph and replayed.
+
+Per layer of a window forward (rows = bs * W):
+    gss_rmsnorm / gss_add_rmsnorm   input norm, or (residual + post-norm) fused with the next norm
+    qkv = x @ Wqkv^T                hipBLASLt through torch.mm (fused q|k|v projection)
+    gss_rope_stage                  rotate q, k; stage the window K/V (not yet in the cache)
+    gss_draft_attn / gss_verify_attn   paged prefix + window, draft or verify mask
+    o_proj, gate_up, down           hipBLASLt
+    gss_silu_mul                    SwiGLU
+A round (the serving full-draft round, patches/sglang/.../selfspec_diffusion_worker.py:660-961):
+    draft forward [x0 | MASK x B] -> gss_argmax_accept (argmax only) -> gss_kv_commit of row 0 (x0)
+    verify forward [a0, d_1..d_B] -> gss_argmax_accept (argmax + accept + bonus) -> gss_kv_commit of acc+1 rows
+"""
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import kernels as K
+from .model import GlmTextConfig
+
+PAGE = K.PAGE
+
+
+class _Bufs:
+    """Activation buffers of one (bs, W) window shape."""
+
+    def __init__(self, eng: "GssEngine", bs: int, W: int):
+        c, dev, bf = eng.cfg, eng.device, torch.bfloat16
+        rows = bs * W
+        self.bs, self.W = bs, W
+        self.h = torch.empty(rows, c.hidden, dtype=bf, device=dev)
+        self.x = torch.empty(rows, c.hidden, dtype=bf, device=dev)
+        self.qkv = torch.empty(rows, c.qkv_dim, dtype=bf, device=dev)
+        self.q = torch.empty(bs, W, c.n_heads, c.head_dim, dtype=bf, device=dev)
+        self.o = torch.empty(bs, W, c.n_heads, c.head_dim, dtype=bf, device=dev)
+        self.a = torch.empty(rows, c.hidden, dtype=bf, device=dev)
+        self.gu = torch.empty(rows, 2 * c.ffn, dtype=bf, device=dev)
+        self.act = torch.empty(rows, c.ffn, dtype=bf, device=dev)
+        self.logits = torch.empty(rows, c.vocab, dtype=bf, device=dev)
+        self.k_win = torch.empty(c.n_layers, bs, W, c.n_kv_heads, c.head_dim, dtype=bf, device=dev)
+        self.v_win = torch.empty_like(self.k_win)
+
+
+class GssEngine:
+    """Weights, paged KV pool and kernels for up to ``max_bs`` sequences of up to ``max_len`` tokens each."""
+
+    def __init__(self, cfg: GlmTextConfig, weights: Dict[str, torch.Tensor], *, max_bs: int, max_len: int,
+                 device="cuda", page_seed: int = 0, max_win: int = 48):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.max_bs, self.max_len, self.max_win = max_bs, max_len, max_win
+        dev, bf = self.device, torch.bfloat16
+
+        def up(t):
+            return t.detach().to(device=dev, dtype=bf).contiguous()
+
+        L = cfg.n_layers
+        self.embed = up(weights["embed"])
+        self.wqkv = [up(torch.cat([weights[f"{l}.wq"], weights[f"{l}.wk"], weights[f"{l}.wv"]], 0)) for l in range(L)]
+        self.wo = [up(weights[f"{l}.wo"]) for l in range(L)]
+        self.wgu = [up(weights[f"{l}.w_gate_up"]) for l in range(L)]
+        self.wdown = [up(weights[f"{l}.w_down"]) for l in range(L)]
+        self.n_in = [up(weights[f"{l}.in_norm"]) for l in range(L)]
+        self.n_psa = [up(weights[f"{l}.post_self_attn_norm"]) for l in range(L)]
+        self.n_pa = [up(weights[f"{l}.post_attn_norm"]) for l in range(L)]
+        self.n_pm = [up(weights[f"{l}.post_mlp_norm"]) for l in range(L)]
+        self.n_final = up(weights["norm"])
+        self.lm_head = up(weights["lm_head"])
+        rot = cfg.rot_dim
+        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2, dtype=torch.int64).float() / rot))).to(dev)
+        self.scale = cfg.head_dim ** -0.5
+
+        # paged KV pool: every sequence slot owns ceil(max_len / 16) pages, drawn from a seeded permutation of the
+        # pool (pages of one sequence are scattered, as a shared serving pool leaves them)
+        self.pages_per_seq = (max_len + PAGE - 1) // PAGE
+        n_pages = max_bs * self.pages_per_seq
+        perm = np.random.default_rng(page_seed).permutation(n_pages).astype(np.int32)
+        self.page_table = torch.from_numpy(perm.reshape(max_bs, self.pages_per_seq)).to(dev)
+        self.k_pages = torch.zeros(L, n_pages, cfg.n_kv_heads, PAGE, cfg.head_dim, dtype=bf, device=dev)
+        self.v_pages = torch.zeros(L, n_pages, cfg.n_kv_heads, cfg.head_dim, PAGE, dtype=bf, device=dev)
+        self.seq_lens = torch.zeros(max_bs, dtype=torch.int32, device=dev)
+
+        self.ws_attn = torch.zeros(max(1, K.attn_workspace_bytes(max_bs, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim,
+                                                                 max_win, max_len)), dtype=torch.uint8, device=dev)
+        self.ws_arg = torch.zeros(K.argmax_workspace_bytes(max_bs, max_win, cfg.vocab), dtype=torch.uint8, device=dev)
+        self.ws_commit = torch.zeros(K.commit_workspace_bytes(max_bs), dtype=torch.uint8, device=dev)
+        self._bufs: Dict[Tuple[int, int], _Bufs] = {}
+
+    # ------------------------------------------------------------------------------------------ primitives ------
+    def bufs(self, bs: int, W: int) -> _Bufs:
+        key = (bs, W)
+        if key not in self._bufs:
+            if bs > self.max_bs or W > self.max_win:
+                raise ValueError(f"window {bs}x{W} exceeds the engine's {self.max_bs}x{self.max_win}")
+            self._bufs[key] = _Bufs(self, bs, W)
+        return self._bufs[key]
+
+    def forward(self, b: _Bufs, *, ids: Optional[torch.Tensor] = None, emb: Optional[torch.Tensor] = None,
+                n_causal: Optional[int], seq_lens: Optional[torch.Tensor] = None,
+                page_table: Optional[torch.Tensor] = None, pos_delta: Optional[torch.Tensor] = None,
+                max_kv_len: Optional[int] = None) -> torch.Tensor:
+        """One window forward of all layers. ``ids`` int32/int64 [bs, W] or ``emb`` [bs*W, H]; n_causal None =
+        verify mask. The window's K/V is left in b.k_win / b.v_win (not committed). Returns logits [bs, W, V]."""
+        c = self.cfg
+        bs, W = b.bs, b.W
+        sl = self.seq_lens[:bs] if seq_lens is None else seq_lens
+        pt = self.page_table[:bs] if page_table is None else page_table
+        mkl = self.max_len if max_kv_len is None else max_kv_len
+        if emb is not None:
+            b.h.copy_(emb.view(bs * W, c.hidden))
+        else:
+            torch.index_select(self.embed, 0, ids.reshape(-1), out=b.h)
+        K.rmsnorm(b.h, self.n_in[0], b.x, c.rms_eps)
+        for l in range(c.n_layers):
+            torch.mm(b.x, self.wqkv[l].t(), out=b.qkv)
+            K.rope_stage(b.qkv, sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], pos_delta=pos_delta,
+                         rot_dim=c.rot_dim)
+            K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
+                               n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
+            torch.mm(b.o.view(bs * W, -1), self.wo[l].t(), out=b.a)
+            K.add_rmsnorm(b.a, self.n_psa[l], b.h, self.n_pa[l], b.x, c.rms_eps)
+            torch.mm(b.x, self.wgu[l].t(), out=b.gu)
+            K.silu_mul(b.gu, b.act)
+            torch.mm(b.act, self.wdown[l].t(), out=b.a)
+            nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
+            K.add_rmsnorm(b.a, self.n_pm[l], b.h, nxt, b.x, c.rms_eps)
+        torch.mm(b.x, self.lm_head.t(), out=b.logits)
+        return b.logits.view(bs, W, c.vocab)
+
+    def commit(self, b: _Bufs, *, n_rows=None, n_add: int = 0, slots=None, seq_lens=None, page_table=None):
+        bs = b.bs
+        K.kv_commit(b.k_win, b.v_win, self.k_pages, self.v_pages,
+                    self.page_table[:bs] if page_table is None else page_table,
+                    self.seq_lens[:bs] if seq_lens is None else seq_lens, self.ws_commit, n_rows=n_rows, n_add=n_add,
+                    slots=slots)
+
+    def argmax(self, logits, target, **kw):
+        K.argmax_accept(logits, target, self.ws_arg, **kw)
+
+    # ------------------------------------------------------------------------------------------ prefill ---------
+    def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 32, pos_delta: Optional[torch.Tensor] = None):
+        """Causal prefill of one sequence slot from its prompt embeddings [P, H] (committed into the pages in
+        chunks of ``chunk`` rows through the verify kernel). Returns the logits of the last prompt row [V]."""
+        P = emb.shape[0]
+        if P > self.max_len:
+            raise ValueError("prompt longer than the engine capacity")
+        sl = self.seq_lens[slot:slot + 1]
+        pt = self.page_table[slot:slot + 1]
+        sl.zero_()
+        emb = emb.to(device=self.device, dtype=torch.bfloat16)
+        last = None
+        for s0 in range(0, P, chunk):
+            n = min(chunk, P - s0)
+            b = self.bufs(1, n)
+            logits = self.forward(b, emb=emb[s0:s0 + n], n_causal=None, seq_lens=sl, page_table=pt,
+                                  pos_delta=pos_delta)
+            self.commit(b, n_add=n, seq_lens=sl, page_table=pt)
+            last = logits[0, n - 1]
+        return last
+
+
+@dataclass
+class RoundState:
+    """Device state of a batch of sequences decoded with the full-draft round (K = B + 1 rows per forward)."""
+    bs: int
+    K: int
+    x0: torch.Tensor          # int32 [bs]   boundary token (committed, its K/V not yet in the cache)
+    win: torch.Tensor         # int32 [bs, K] draft window [x0 | MASK x B]
+    am: torch.Tensor          # int32 [bs, K] draft argmax = verify window [a0, d_1..d_B]
+    tgt: torch.Tensor         # int32 [bs, K] verify argmax
+    acc: torch.Tensor         # int32 [bs]
+    packed: torch.Tensor      # int32 [bs, K+2] (a0, acc, targets zeroed past acc)
+    slots: torch.Tensor       # int32 [bs, K]  paged slots of the committed verify rows
+    log: torch.Tensor         # int32 [max_rounds, bs, K+2] packed rows of every round
+    ctr: torch.Tensor         # int64 [1] rounds logged
+    graph: Optional[torch.cuda.CUDAGraph] = None
+
+
+class SelfSpecDecoder:
+    """The full-draft self-spec round and the AR step over a GssEngine, device resident and graph-capturable."""
+
+    def __init__(self, eng: GssEngine, bd: int, mask_id: int, bs: int = 1, max_rounds: int = 4096):
+        self.eng, self.bd, self.mask_id, self.bs = eng, bd, mask_id, bs
+        Kw = bd + 1
+        dev = eng.device
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.st = RoundState(bs=bs, K=Kw, x0=torch.zeros(bs, **i32), win=torch.full((bs, Kw), mask_id, **i32),
+                             am=torch.zeros(bs, Kw, **i32), tgt=torch.zeros(bs, Kw, **i32),
+                             acc=torch.zeros(bs, **i32), packed=torch.zeros(bs, Kw + 2, **i32),
+                             slots=torch.zeros(bs, Kw, **i32), log=torch.zeros(max_rounds, bs, Kw + 2, **i32),
+                             ctr=torch.zeros(1, dtype=torch.int64, device=dev))
+        self.draft_b = eng.bufs(bs, Kw)
+        self.verify_b = _Bufs(eng, bs, Kw)          # separate staging from the draft's
+        self.ar_b = eng.bufs(bs, 1)
+        self.ar_tgt = torch.zeros(bs, 1, **i32)
+        self.ar_log = torch.zeros(max_rounds, bs, **i32)
+        self.ar_ctr = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.g_round = None
+        self.g_ar = None
+
+    # ---- one round, all device-side --------------------------------------------------------------------------
+    def round(self):
+        e, s = self.eng, self.st
+        s.win[:, 0].copy_(s.x0)
+        lg = e.forward(self.draft_b, ids=s.win, n_causal=1)
+        e.argmax(lg, s.am)                                                  # a0, d_1..d_B
+        e.commit(self.draft_b, n_add=1)                                     # x0's K/V (causal row 0): S += 1
+        lg = e.forward(self.verify_b, ids=s.am, n_causal=None)
+        e.argmax(lg, s.tgt, window=s.am, accept_len=s.acc, next_x0=s.x0, packed=s.packed)
+        e.commit(self.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)       # a0, d_1..d_acc: S += acc + 1
+        s.log.index_copy_(0, s.ctr, s.packed.unsqueeze(0))
+        s.ctr.add_(1)
+
+    def ar_step(self):
+        e = self.eng
+        lg = e.forward(self.ar_b, ids=self.st.x0.view(self.bs, 1), n_causal=None)
+        e.argmax(lg, self.ar_tgt)
+        e.commit(self.ar_b, n_add=1)
+        self.st.x0.copy_(self.ar_tgt[:, 0])
+        self.ar_log.index_copy_(0, self.ar_ctr, self.ar_tgt.view(1, self.bs))
+        self.ar_ctr.add_(1)
+
+    def capture(self):
+        """Capture one round and one AR step as HIP graphs (call after one eager warm-up of each)."""
+        self.g_round = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.g_round):
+            self.round()
+        self.g_ar = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.g_ar):
+            self.ar_step()
+
+    def start(self, x0: torch.Tensor):
+        """Begin decoding: x0 = the token the prefill produced (committed; no K/V yet)."""
+        self.st.x0.copy_(x0.to(torch.int32))
+        self.st.ctr.zero_()
+        self.ar_ctr.zero_()
+
+    # ---- host views -------------------------------------------------------------------------------------------
+    def committed(self, n_rounds: int) -> List[List[int]]:
+        """Committed ids per sequence over the first n_rounds logged rounds: [a0, t_0..t_acc] per round."""
+        log = self.st.log[:n_rounds].cpu().numpy()
+        out = [[] for _ in range(self.bs)]
+        for r in range(n_rounds):
+            for b in range(self.bs):
+                a = int(log[r, b, 1])
+                out[b].append(int(log[r, b, 0]))
+                out[b].extend(int(x) for x in log[r, b, 2:3 + a])
+        return out
+
+    def accept_lengths(self, n_rounds: int) -> np.ndarray:
+        return self.st.log[:n_rounds, :, 1].cpu().numpy()

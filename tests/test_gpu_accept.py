@@ -31,7 +31,8 @@ def make_case(bs, W, V, seed, near_tie_frac=0.01, dtype=torch.bfloat16):
         m = min(int(g.geometric(0.1)) - 1, W - 1)        # number of leading matches
         window[b, 0] = g.integers(0, V)
         for r in range(W - 1):
-            window[b, r + 1] = tgt[b, r] if r < m else (tgt[b, r] + 1 + g.integers(0, V - 1)) % V
+            wrong = (tgt[b, r] + 1 + g.integers(0, V - 1)) % V if V > 1 else tgt[b, r]  # V = 1: no other id
+            window[b, r + 1] = tgt[b, r] if r < m else wrong
     return logits, window, tgt
 
 

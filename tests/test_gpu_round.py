@@ -1,0 +1,163 @@
+"""The full-draft round on the GPU (bf16, HIP kernels + hipBLASLt GEMMs) on the tiny plumbing decoder and a
+mid-size decoder:
+  * prefill logits match the fp32 oracle within the bf16 tolerance;
+  * one round's draft/verify logits match the oracle round on the same state;
+  * committed ids equal the GPU's own AR greedy decode, except at argmax near-ties (AR top-2 gap < 1e-3 for the
+    first divergent token), and the KV committed by the rounds equals the KV an AR decode writes;
+  * HIP-graph replay of the round reproduces the eager rounds exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.decoder import TINY as O_TINY, OracleDecoder, make_prefix, make_weights
+from oracle.rounds import ar_generate, fulldraft_generate, prefill as o_prefill
+from tests.helpers import LOGIT_ABS
+
+pytestmark = pytest.mark.gpu
+
+NEAR_TIE = 1e-3
+
+
+def build(dev, cfg, seed, n_vis, n_text, bd, max_len, mask_id=None):
+    from gravityocr_amd.engine import GssEngine, SelfSpecDecoder
+    from gravityocr_amd.model import synthetic_prompt, synthetic_weights
+    w = synthetic_weights(cfg, seed)
+    vis, ids = synthetic_prompt(cfg, n_vis, n_text, seed)
+    eng = GssEngine(cfg, w, max_bs=1, max_len=max_len, device=dev)
+    emb = torch.cat([vis, w["embed"][ids]], 0)
+    dec = SelfSpecDecoder(eng, bd=bd, mask_id=cfg.vocab - 1 if mask_id is None else mask_id, bs=1)
+    return eng, dec, w, emb
+
+
+def gpu_ar(eng, dec, emb, n):
+    last = eng.prefill(0, emb)
+    x0 = last.float().argmax().view(1)
+    dec.start(x0)
+    toks = [int(x0)]
+    logits = [last.float().cpu()]
+    for _ in range(n - 1):
+        lg = eng.forward(dec.ar_b, ids=dec.st.x0.view(1, 1), n_causal=None)
+        logits.append(lg[0, 0].float().cpu())
+        eng.argmax(lg, dec.ar_tgt)
+        eng.commit(dec.ar_b, n_add=1)
+        dec.st.x0.copy_(dec.ar_tgt[:, 0])
+        toks.append(int(dec.ar_tgt[0, 0]))
+    return toks, logits
+
+
+def gpu_spec(eng, dec, emb, n_min, graph=False):
+    last = eng.prefill(0, emb)
+    x0 = last.float().argmax().view(1)
+    dec.start(x0)
+    out = [int(x0)]
+    rounds = 0
+    while len(out) < n_min:
+        if graph:
+            dec.g_round.replay()
+        else:
+            dec.round()
+        rounds += 1
+        out = [int(x0)] + dec.committed(rounds)[0]
+    return out, rounds
+
+
+def first_divergence(a, b):
+    for i, (x, y) in enumerate(zip(a, b)):
+        if x != y:
+            return i
+    return None
+
+
+def top2_gap(row):
+    v = torch.topk(row.float(), 2).values
+    return float(v[0] - v[1])
+
+
+def test_tiny_prefill_logits_match_oracle(cuda):
+    from gravityocr_amd.model import TINY
+    eng, dec, w, emb = build(cuda, TINY, 0, 256, 16, 4, 512)
+    last = eng.prefill(0, emb).float().cpu()
+    # oracle on the same bf16-rounded weights and inputs, computed in fp32
+    wb = {k: v.bfloat16().float() for k, v in w.items()}
+    o = OracleDecoder(O_TINY, wb)
+    _, ref = o_prefill(o, emb.bfloat16().float())
+    err = float((last - ref[0]).abs().max())
+    print("tiny prefill logits max abs err", err, "ref scale", float(ref.abs().max()))
+    assert err <= LOGIT_ABS
+
+
+@pytest.mark.parametrize("cfg_name,bd,n_tok", [("tiny", 4, 96), ("mid", 16, 160)])
+def test_spec_equals_ar_on_gpu(cuda, cfg_name, bd, n_tok):
+    from gravityocr_amd.model import TINY, GlmTextConfig
+    cfg = TINY if cfg_name == "tiny" else GlmTextConfig(n_layers=4, hidden=1536, n_heads=16, n_kv_heads=2,
+                                                        head_dim=128, ffn=4608, vocab=59392)
+    n_vis = 256 if cfg_name == "tiny" else 1000
+    eng, dec, w, emb = build(cuda, cfg, 2, n_vis, 16, bd, 2048)
+    ar, ar_logits = gpu_ar(eng, dec, emb, n_tok + bd + 2)
+    spec, rounds = gpu_spec(eng, dec, emb, n_tok)
+    accs = dec.accept_lengths(rounds)[:, 0]
+    print(f"{cfg_name}: {len(spec)} tokens in {rounds} rounds, mean committed/round {(len(spec) - 1) / rounds:.2f}",
+          "accept hist", np.bincount(accs, minlength=bd + 1).tolist())
+    i = first_divergence(spec, ar)
+    if i is not None:
+        gap = top2_gap(ar_logits[i])
+        print(f"first divergence at {i}: spec {spec[i]} ar {ar[i]} AR top-2 gap {gap}")
+        assert gap < NEAR_TIE, (i, gap)
+    assert len(spec) >= n_tok
+
+
+def test_kv_committed_by_rounds_equals_ar_kv(cuda):
+    from gravityocr_amd.model import TINY
+    eng, dec, w, emb = build(cuda, TINY, 3, 256, 16, 4, 1024)
+    ar, _ = gpu_ar(eng, dec, emb, 60)
+    P = emb.shape[0]
+    n_ar = int(eng.seq_lens[0])
+    kv_ar = [eng.k_pages.clone(), eng.v_pages.clone()]
+    spec, rounds = gpu_spec(eng, dec, emb, 40)
+    n_sp = int(eng.seq_lens[0])
+    assert n_sp == len(spec) - 1 + P          # every committed token but the boundary one has K/V
+    if first_divergence(spec, ar) is None:
+        n = min(n_ar, n_sp)
+        pt = eng.page_table[0].cpu().numpy()
+        for pos in range(P, n):
+            pg, o = int(pt[pos // 16]), pos % 16
+            ka, ks = kv_ar[0][:, pg, :, o].float(), eng.k_pages[:, pg, :, o].float()
+            # same token ids and prefix: the rounds' verify rows and AR's single rows differ only by GEMM shape
+            assert float((ka - ks).abs().max()) <= 0.05 * float(ka.abs().max()) + 1e-3, pos
+
+
+def test_graph_replay_matches_eager(cuda):
+    from gravityocr_amd.model import TINY
+    eng, dec, w, emb = build(cuda, TINY, 4, 256, 16, 4, 1024)
+    eager, r1 = gpu_spec(eng, dec, emb, 50)
+    # warm-up done by the eager rounds; capture from a fresh prefill state
+    eng.prefill(0, emb)
+    dec.round()
+    dec.ar_step()
+    dec.capture()
+    for rep in range(2):   # replays separated by eager work and syncs, each checked against the eager result
+        graphed, r2 = gpu_spec(eng, dec, emb, 50, graph=True)
+        torch.cuda.synchronize()
+        assert graphed == eager and r1 == r2, rep
+
+
+def test_mid_round_logits_match_oracle_round(cuda):
+    """One round's draft and verify logits (GPU bf16) vs the oracle round (fp32, same bf16 weights/inputs)."""
+    from gravityocr_amd.model import TINY
+    eng, dec, w, emb = build(cuda, TINY, 5, 256, 16, 4, 1024)
+    last = eng.prefill(0, emb)
+    dec.start(last.float().argmax().view(1))
+    dec.round()
+    torch.cuda.synchronize()
+    d_logits = dec.draft_b.logits.float().cpu()
+    v_logits = dec.verify_b.logits.float().cpu()
+    wb = {k: v.bfloat16().float() for k, v in w.items()}
+    o = OracleDecoder(O_TINY, wb)
+    trace = []
+    out, rounds = fulldraft_generate(o, emb.bfloat16().float(), 4, TINY.vocab - 1, 2, trace=trace)
+    assert out[0] == int(last.float().argmax())
+    ed = float((d_logits - trace[0]["draft_logits"]).abs().max())
+    ev = float((v_logits - trace[0]["verify_logits"]).abs().max())
+    print("round logits err draft", ed, "verify", ev)
+    assert ed <= LOGIT_ABS and ev <= LOGIT_ABS
