@@ -1,0 +1,301 @@
+"""Headline benchmark: bs=1 self-speculative decode on one MI355X.
+
+Workload: the 16-layer, 1536-hidden GLM decoder (16 q / 2 kv heads, head_dim 128, SwiGLU 4608, vocab 59392, bf16,
+random N(0, 0.02) weights, seed 2); prompt = 2048 visual embeddings N(0,1) + 6144 text ids U[0, vocab) (the first
+32 are the prompt, the rest fill the KV prefix to 8K), prefilled (untimed) into 16-token pages; then full-draft rounds
+with B = 16 (K = 17 rows per forward: draft forward + verify forward + argmax/accept/bonus + KV commit) until 512
+tokens are committed. A "step" is one round. Each round is one HIP-graph replay; lengths live on the device.
+
+Reported next to it, in the same JSON line:
+  * AR decode of the same model on the same GPU (one 1-row forward per token, also graph-replayed);
+  * planted-acceptance rounds: the draft is overwritten with the AR tokens up to a mismatch ~ geometric(0.1)
+    (capped at B), so the verify accepts what a trained draft would (kernel cost per round does not depend on it);
+  * roofline of the block-diffusion draft attention kernel at the round's shape (HIP events on its stream);
+  * the CPU baseline: the oracle's full-draft round (fp32 torch) on the host cores, from the same 8K state.
+
+    python bench.py [--steps K] [--warmup W] [--no-cpu] [--prefix 8192] [--tokens 512] [--bd 16]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def attn_bytes(L, W, Hq=16, Hkv=2, D=128):
+    """algorithmic HBM bytes of one window-attention call: K and V of L+W tokens + Q and O of W rows (bf16)."""
+    return 2 * Hkv * D * 2 * (L + W) + 2 * W * Hq * D * 2
+
+
+def attn_flops(L, W, Hq=16, D=128):
+    return 4 * W * Hq * D * (L + W)
+
+
+def time_kernel(fn, n=100, reps=5):
+    """average duration of one fn() launch: n launches captured back to back in one HIP graph (no host work between
+    them), replayed ``reps`` times between HIP events on the capture/launch stream; returns microseconds."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (n * reps)  # us
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=0, help="timed rounds (0 = the rounds that commit --tokens)")
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--prefix", type=int, default=8192)
+    ap.add_argument("--tokens", type=int, default=512)
+    ap.add_argument("--bd", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--profile-only", action="store_true", help="skip AR, planted and CPU legs (for rocprof runs)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the self-spec round shards by sequence (no collective), so a multi-GPU "
+              "figure is N independent copies of this one; run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    from gravityocr_amd.engine import GssEngine, SelfSpecDecoder
+    from gravityocr_amd.model import SYNTH_1536 as cfg, synthetic_prompt, synthetic_weights
+    from gravityocr_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    bd, Kw, P = args.bd, args.bd + 1, args.prefix
+    t0 = time.time()
+    w = synthetic_weights(cfg, seed=2)
+    vis, ids = synthetic_prompt(cfg, 2048, P - 2048, seed=2)
+    emb = torch.cat([vis, w["embed"][ids]], 0)
+    log(f"weights + prompt drawn in {time.time() - t0:.1f}s")
+    max_len = P + args.tokens + 4 * (Kw + 1) + 64
+    eng = GssEngine(cfg, w, max_bs=1, max_len=max_len, device=dev)
+    mask_id = cfg.vocab - 1
+    # logs: one row per round / AR step; the AR leg runs warmup + tokens + K + 2 steps
+    dec = SelfSpecDecoder(eng, bd=bd, mask_id=mask_id, bs=1,
+                          max_rounds=max(args.steps, args.tokens + Kw + 2) + args.warmup + 8)
+    t0 = time.time()
+    last = eng.prefill(0, emb)
+    torch.cuda.synchronize()
+    prefill_s = time.time() - t0
+    x00 = last.float().argmax().view(1)
+    log(f"prefill of {P} tokens: {prefill_s:.2f}s; first token {int(x00)}")
+
+    def reset():
+        eng.seq_lens[:1].fill_(P)
+        dec.start(x00)
+
+    # ---- warm up eagerly, capture the round and the AR step as HIP graphs ----------------------------------------
+    reset()
+    dec.round()
+    reset()
+    dec.ar_step()
+    reset()
+    dec.capture()
+    torch.cuda.synchronize()
+    log("graphs captured")
+
+    # ---- AR baseline: args.tokens AR steps, graph-replayed --------------------------------------------------------
+    ar_tps = ar_us = None
+    ar_tokens = None
+    if not args.profile_only:
+        n_ar = args.tokens + Kw + 2
+        reset()
+        for _ in range(args.warmup):
+            dec.g_ar.replay()
+        reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n_ar):
+            dec.g_ar.replay()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        ar_tps, ar_us = n_ar / dt, dt / n_ar * 1e6
+        ar_tokens = [int(x00)] + dec.ar_log[:n_ar, 0].cpu().tolist()
+        log(f"AR: {ar_tps:.1f} tokens/s ({ar_us:.1f} us/token)")
+
+    # ---- calibration: rounds that commit args.tokens (untimed) ---------------------------------------------------
+    reset()
+    rounds = 0
+    committed = 1
+    while committed < args.tokens:
+        dec.g_round.replay()
+        rounds += 1
+        committed += int(dec.st.packed[0, 1]) + 2
+    steps = args.steps if args.steps > 0 else rounds
+    log(f"calibration: {rounds} rounds commit {committed} tokens; timing {steps} rounds")
+
+    # ---- timed spec rounds ------------------------------------------------------------------------------------
+    reset()
+    for _ in range(args.warmup):
+        dec.g_round.replay()
+    reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        dec.g_round.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    accs = dec.accept_lengths(steps)[:, 0]
+    n_commit = int((accs + 2).sum())
+    spec_tokens = [int(x00)] + dec.committed(steps)[0]
+    tps = n_commit / dt
+    round_us = dt / steps * 1e6
+    log(f"spec: {n_commit} tokens in {steps} rounds, {tps:.1f} tokens/s, {round_us:.1f} us/round")
+    match = None
+    if ar_tokens is not None:
+        n = min(len(ar_tokens), len(spec_tokens))
+        match = next((i for i in range(n) if ar_tokens[i] != spec_tokens[i]), n)
+
+    # ---- draft / verify halves (eager launches of the same kernels, graph-free timing) -------------------------
+    # ---- planted acceptance ---------------------------------------------------------------------------------
+    planted = None
+    if ar_tokens is not None:
+        g = np.random.default_rng(7)
+        m_draw = np.minimum(g.geometric(0.1, size=args.tokens + 8) - 1, bd)
+        ar_dev = torch.tensor(ar_tokens + [0] * (Kw + 2), dtype=torch.int32, device=dev)
+        m_dev = torch.tensor(m_draw, dtype=torch.int64, device=dev)
+        jj = torch.arange(1, Kw, device=dev)
+
+        def plant():
+            st = dec.st
+            base = (eng.seq_lens[:1].long() - P)                      # after the x0 commit: a0's AR index
+            idx = (base[:, None] + jj[None, :]).clamp(max=ar_dev.numel() - 1)
+            good = ar_dev[idx]
+            m = m_dev[st.ctr.clamp(max=m_dev.numel() - 1)]            # this round's planted match count
+            bad = (good + 1) % cfg.vocab
+            st.am[:, 1:] = torch.where(jj[None, :] <= m[:, None], good, bad)
+
+        gp = torch.cuda.CUDAGraph()
+        reset()
+        dec.round(after_draft=plant)
+        reset()
+        with torch.cuda.graph(gp):
+            dec.round(after_draft=plant)
+        reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pr = 0
+        pc = 1
+        while pc < args.tokens:
+            gp.replay()
+            pr += 1
+            pc += int(dec.st.packed[0, 1]) + 2
+        torch.cuda.synchronize()
+        pdt = time.perf_counter() - t0
+        paccs = dec.accept_lengths(pr)[:, 0]
+        ptoks = [int(x00)] + dec.committed(pr)[0]
+        n = min(len(ptoks), len(ar_tokens))
+        planted = {"tokens_per_s": round(int((paccs + 2).sum()) / pdt, 1), "rounds": pr,
+                   "mean_committed_per_round": round(float((paccs + 2).mean()), 3),
+                   "speedup_vs_ar": round((int((paccs + 2).sum()) / pdt) / ar_tps, 3),
+                   "ids_equal_ar_prefix": next((i for i in range(n) if ptoks[i] != ar_tokens[i]), n),
+                   "note": "timing includes one host readback per round (loop control)"}
+        log(f"planted: {planted}")
+
+    # ---- draft attention roofline at the round's shape -----------------------------------------------------------
+    L = P + args.tokens // 2
+    b = dec.draft_b
+    sl = torch.tensor([L], dtype=torch.int32, device=dev)
+
+    def draft_attn():
+        K.window_attention(b.q, eng.k_pages[0], eng.v_pages[0], eng.page_table[:1], sl, b.k_win[0], b.v_win[0], b.o,
+                           n_causal=1, scale=eng.scale, max_kv_len=eng.max_len, workspace=eng.ws_attn)
+
+    def verify_attn():
+        K.window_attention(b.q, eng.k_pages[0], eng.v_pages[0], eng.page_table[:1], sl, b.k_win[0], b.v_win[0], b.o,
+                           n_causal=None, scale=eng.scale, max_kv_len=eng.max_len, workspace=eng.ws_attn)
+
+    d_us = time_kernel(draft_attn)
+    v_us = time_kernel(verify_attn)
+    ab = attn_bytes(L, Kw)
+    achieved = ab / (d_us * 1e-6) / 1e9
+    tflops = attn_flops(L, Kw) / (d_us * 1e-6) / 1e12
+    log(f"draft attention L={L}: {d_us:.2f} us, {achieved:.0f} GB/s, {tflops:.1f} TFLOP/s; verify {v_us:.2f} us")
+
+    # ---- CPU baseline: the oracle's round on the host cores, from the same 8K state -----------------------------
+    cpu = None
+    if not args.no_cpu and not args.profile_only:
+        from oracle.decoder import DecoderConfig, KVCache, OracleDecoder
+        from oracle.rounds import fulldraft_round
+        torch.set_num_threads(os.cpu_count() or 1)
+        ocfg = DecoderConfig(n_layers=cfg.n_layers, hidden=cfg.hidden, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
+                             head_dim=cfg.head_dim, ffn=cfg.ffn, vocab=cfg.vocab)
+        wb = {k: v.bfloat16().float() for k, v in w.items()}
+        om = OracleDecoder(ocfg, wb)
+        reset()
+        pt = eng.page_table[0, : (P + 15) // 16].long()
+        cache = KVCache(cfg.n_layers)
+        for l in range(cfg.n_layers):
+            kk = eng.k_pages[l][pt].permute(0, 2, 1, 3).reshape(-1, cfg.n_kv_heads, cfg.head_dim)[:P]
+            vv = eng.v_pages[l][pt].permute(0, 3, 1, 2).reshape(-1, cfg.n_kv_heads, cfg.head_dim)[:P]
+            cache.append(l, kk.float().cpu(), vv.float().cpu())
+        S, x0 = P, int(x00)
+        fulldraft_round(om, cache, S, x0, bd, mask_id)      # warm-up (not counted), state restored below
+        cache.truncate(P)
+        n_r = n_t = 0
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            while time.perf_counter() - t0 < args.cpu_seconds or n_r < 2:
+                S, x0, T, acc, _ = fulldraft_round(om, cache, S, x0, bd, mask_id)
+                n_r += 1
+                n_t += len(T)
+        cdt = time.perf_counter() - t0
+        cpu = {"value": round(n_t / cdt, 3), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{n_r} full-draft rounds (B={bd}) of the fp32 oracle from the same {P}-token state, "
+                         f"{cdt:.1f}s", "round_ms": round(cdt / n_r * 1e3, 1)}
+        log(f"CPU baseline: {cpu}")
+
+    round_bytes = 2 * (1_088_618_496 + 16 * 1024 * (L + Kw) + Kw * cfg.vocab * 2)
+    out = {
+        "metric": "committed tokens/s bs=1 + draft/verify round µs; attn HBM GB/s vs peak",
+        "value": round(tps, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(round_us / 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (random-init weights, seeded N(0,1) visual embeddings and U[0,V) ids)",
+        "config": {"workload": f"bs=1 self-spec full-draft rounds, 16-layer 1536-hidden GLM decoder, {P}-token "
+                               f"prefix, B={bd}, {args.tokens} committed tokens", "bs": 1, "prefix": P, "bd": bd,
+                   "K": Kw, "tokens": args.tokens, "parallelism": "none (one GPU)"},
+        "round_us": round(round_us, 1),
+        "mean_committed_per_round": round(n_commit / steps, 3),
+        "accept_hist": np.bincount(accs, minlength=bd + 1).tolist(),
+        "ar_tokens_per_s": None if ar_tps is None else round(ar_tps, 2),
+        "ar_us_per_token": None if ar_us is None else round(ar_us, 1),
+        "speedup_vs_ar": None if ar_tps is None else round(tps / ar_tps, 3),
+        "spec_equals_ar_prefix": match,
+        "planted": planted,
+        "round_hbm_frac": round(round_bytes / (round_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "prefill_s": round(prefill_s, 2),
+        "roofline": {"bound": "hbm", "kernel": "gss_draft_attn (block-diffusion draft attention)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": ab, "avg_us": round(d_us, 2), "L": L, "W": Kw,
+                     "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "verify_avg_us": round(v_us, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

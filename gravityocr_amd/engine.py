@@ -143,25 +143,49 @@ class GssEngine:
         K.argmax_accept(logits, target, self.ws_arg, **kw)
 
     # ------------------------------------------------------------------------------------------ prefill ---------
-    def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 32, pos_delta: Optional[torch.Tensor] = None):
-        """Causal prefill of one sequence slot from its prompt embeddings [P, H] (committed into the pages in
-        chunks of ``chunk`` rows through the verify kernel). Returns the logits of the last prompt row [V]."""
+    def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 48, pos_delta: Optional[torch.Tensor] = None):
+        """Causal prefill of one sequence slot from its prompt embeddings [P, H]: whole-prompt GEMMs, attention in
+        causal chunks of ``chunk`` rows through the verify kernel (prefix from the pages, chunk as the window),
+        K/V committed layer by layer. Returns the logits of the last prompt row [V] (bf16)."""
+        c, dev, bf = self.cfg, self.device, torch.bfloat16
         P = emb.shape[0]
         if P > self.max_len:
             raise ValueError("prompt longer than the engine capacity")
-        sl = self.seq_lens[slot:slot + 1]
         pt = self.page_table[slot:slot + 1]
-        sl.zero_()
-        emb = emb.to(device=self.device, dtype=torch.bfloat16)
-        last = None
-        for s0 in range(0, P, chunk):
-            n = min(chunk, P - s0)
-            b = self.bufs(1, n)
-            logits = self.forward(b, emb=emb[s0:s0 + n], n_causal=None, seq_lens=sl, page_table=pt,
-                                  pos_delta=pos_delta)
-            self.commit(b, n_add=n, seq_lens=sl, page_table=pt)
-            last = logits[0, n - 1]
-        return last
+        h = emb.to(device=dev, dtype=bf).contiguous().clone()
+        x = torch.empty_like(h)
+        qkv = torch.empty(P, c.qkv_dim, dtype=bf, device=dev)
+        q = torch.empty(1, P, c.n_heads, c.head_dim, dtype=bf, device=dev)
+        o = torch.empty_like(q)
+        kw = torch.empty(1, 1, P, c.n_kv_heads, c.head_dim, dtype=bf, device=dev)
+        vw = torch.empty_like(kw)
+        a = torch.empty(P, c.hidden, dtype=bf, device=dev)
+        zero = torch.zeros(1, dtype=torch.int32, device=dev)
+        starts = torch.arange(0, P, chunk, dtype=torch.int32, device=dev)
+        lens = torch.zeros(1, dtype=torch.int32, device=dev)
+        K.rmsnorm(h, self.n_in[0], x, c.rms_eps)
+        for l in range(c.n_layers):
+            torch.mm(x, self.wqkv[l].t(), out=qkv)
+            K.rope_stage(qkv, zero, self.inv_freq, q, kw[0], vw[0], pos_delta=pos_delta, rot_dim=c.rot_dim)
+            lens.zero_()
+            K.kv_commit(kw, vw, self.k_pages[l:l + 1], self.v_pages[l:l + 1], pt, lens, self.ws_commit, n_add=P)
+            for i, s0 in enumerate(range(0, P, chunk)):
+                n = min(chunk, P - s0)
+                K.window_attention(q[:, s0:s0 + n].contiguous(), self.k_pages[l], self.v_pages[l], pt,
+                                   starts[i:i + 1], kw[0, :, s0:s0 + n].contiguous(), vw[0, :, s0:s0 + n].contiguous(),
+                                   o[:, s0:s0 + n], n_causal=None, scale=self.scale, max_kv_len=self.max_len,
+                                   workspace=self.ws_attn)
+            torch.mm(o.view(P, -1), self.wo[l].t(), out=a)
+            K.add_rmsnorm(a, self.n_psa[l], h, self.n_pa[l], x, c.rms_eps)
+            gu = torch.mm(x, self.wgu[l].t())
+            act = torch.empty(P, c.ffn, dtype=bf, device=dev)
+            K.silu_mul(gu, act)
+            del gu
+            torch.mm(act, self.wdown[l].t(), out=a)
+            nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
+            K.add_rmsnorm(a, self.n_pm[l], h, nxt, x, c.rms_eps)
+        self.seq_lens[slot:slot + 1].fill_(P)
+        return (x[P - 1:P] @ self.lm_head.t())[0]
 
 
 @dataclass
@@ -204,16 +228,21 @@ class SelfSpecDecoder:
         self.g_ar = None
 
     # ---- one round, all device-side --------------------------------------------------------------------------
-    def round(self):
+    def round(self, after_draft=None):
+        """One full-draft round. ``after_draft`` (optional, device ops only) runs between the x0 commit and the
+        verify forward and may rewrite the verify window ``st.am[:, 1:]`` (the planted-acceptance measurement)."""
         e, s = self.eng, self.st
         s.win[:, 0].copy_(s.x0)
         lg = e.forward(self.draft_b, ids=s.win, n_causal=1)
         e.argmax(lg, s.am)                                                  # a0, d_1..d_B
         e.commit(self.draft_b, n_add=1)                                     # x0's K/V (causal row 0): S += 1
+        if after_draft is not None:
+            after_draft()
         lg = e.forward(self.verify_b, ids=s.am, n_causal=None)
         e.argmax(lg, s.tgt, window=s.am, accept_len=s.acc, next_x0=s.x0, packed=s.packed)
         e.commit(self.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)       # a0, d_1..d_acc: S += acc + 1
-        s.log.index_copy_(0, s.ctr, s.packed.unsqueeze(0))
+        # the log index is clamped on the device, so rounds beyond the log's capacity rewrite its last row
+        s.log.index_copy_(0, s.ctr.clamp(max=s.log.shape[0] - 1), s.packed.unsqueeze(0))
         s.ctr.add_(1)
 
     def ar_step(self):
@@ -222,7 +251,7 @@ class SelfSpecDecoder:
         e.argmax(lg, self.ar_tgt)
         e.commit(self.ar_b, n_add=1)
         self.st.x0.copy_(self.ar_tgt[:, 0])
-        self.ar_log.index_copy_(0, self.ar_ctr, self.ar_tgt.view(1, self.bs))
+        self.ar_log.index_copy_(0, self.ar_ctr.clamp(max=self.ar_log.shape[0] - 1), self.ar_tgt.view(1, self.bs))
         self.ar_ctr.add_(1)
 
     def capture(self):

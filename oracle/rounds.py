@@ -109,43 +109,47 @@ def natcache_generate(model: OracleDecoder, prefix_emb: torch.Tensor, bd: int, m
     return gen, stats
 
 
-def fulldraft_generate(model: OracleDecoder, prefix_emb: torch.Tensor, bd: int, mask_id: int, max_new_tokens: int,
-                       eos_id: Optional[int] = None, pos_offset: int = 0, trace: Optional[list] = None):
-    """The serving full-draft round (patches/sglang/.../selfspec_diffusion_worker.py:660-961 with
-    selfspec_fast_commit.py:108-147), K = bd + 1 rows per forward, AR-aligned positions (SELFSPEC_POS_OFFSET=0).
-
-    The prefill emits x0 (the extend step's sampled token, committed). Each round:
+def fulldraft_round(model: OracleDecoder, cache: KVCache, S: int, x0: int, bd: int, mask_id: int,
+                    pos_offset: int = 0, trace: Optional[list] = None):
+    """One serving full-draft round (patches/sglang/.../selfspec_diffusion_worker.py:660-961 with
+    selfspec_fast_commit.py:108-147), K = bd + 1 rows per forward, AR-aligned positions (SELFSPEC_POS_OFFSET=0):
       draft  [x0 | MASK x bd] at positions S+pos_offset.. (x0 row causal, mask rows bidirectional); am = argmax.
       x0's K/V (draft row 0, causal, exact) is committed: S += 1.
       verify [a0, d_1..d_bd] = am at positions S.. (causal); t = argmax; acc = leading matches t_r == d_{r+1}.
       commit T = [a0, t_0..t_acc]; keep verify K/V rows 0..acc: S += acc + 1; x0 = t_acc.
-    Returns (committed ids, per-round list of dicts {acc, window, target, T, slots_from}).
-    """
+    ``cache`` holds exactly S committed positions on entry and S' on return. Returns (S', x0', T, acc, record)."""
     K = bd + 1
+    ids = torch.tensor([x0] + [mask_id] * bd)
+    cache.truncate(S)
+    dl = model.logits(model.forward(model.embed(ids), torch.arange(S, S + K) + pos_offset, cache,
+                                    window_mask(S, K, 1)))
+    am = dl.float().argmax(-1)                                           # [K] = a0, d_1..d_bd
+    cache.truncate(S + 1)                                                # x0 committed from draft row 0
+    S1 = S + 1
+    vl = model.logits(model.forward(model.embed(am), torch.arange(S1, S1 + K) + pos_offset, cache,
+                                    window_mask(S1, K, K)))
+    t = vl.float().argmax(-1)
+    acc = int(accept_chain(am[None].numpy(), t[None].numpy())[0])
+    T = [int(am[0])] + [int(x) for x in t[: acc + 1]]
+    cache.truncate(S1 + acc + 1)
+    if trace is not None:
+        trace.append({"draft_logits": dl, "verify_logits": vl})
+    rec = {"S": S, "acc": acc, "window": am.tolist(), "target": t.tolist(), "T": T}
+    return S1 + acc + 1, int(t[acc]), T, acc, rec
+
+
+def fulldraft_generate(model: OracleDecoder, prefix_emb: torch.Tensor, bd: int, mask_id: int, max_new_tokens: int,
+                       eos_id: Optional[int] = None, pos_offset: int = 0, trace: Optional[list] = None):
+    """Prefill, then full-draft rounds until max_new_tokens are committed (or EOS). The prefill emits x0 (the
+    extend step's sampled token, committed). Returns (committed ids, per-round records)."""
     cache, last = prefill(model, prefix_emb)
     x0 = int(greedy(last)[0])
     S = prefix_emb.shape[0]
     out = [x0]
     rounds = []
     while len(out) < max_new_tokens and not (eos_id is not None and eos_id in out):
-        ids = torch.tensor([x0] + [mask_id] * bd)
-        cache.truncate(S)
-        dl = model.logits(model.forward(model.embed(ids), torch.arange(S, S + K) + pos_offset, cache,
-                                        window_mask(S, K, 1)))
-        am = dl.float().argmax(-1)                                           # [K] = a0, d_1..d_bd
-        cache.truncate(S + 1)                                                # x0 committed from draft row 0
-        S1 = S + 1
-        vl = model.logits(model.forward(model.embed(am), torch.arange(S1, S1 + K) + pos_offset, cache,
-                                        window_mask(S1, K, K)))
-        t = vl.float().argmax(-1)
-        acc = int(accept_chain(am[None].numpy(), t[None].numpy())[0])
-        T = [int(am[0])] + [int(x) for x in t[: acc + 1]]
-        cache.truncate(S1 + acc + 1)
-        rounds.append({"S": S, "acc": acc, "window": am.tolist(), "target": t.tolist(), "T": T})
-        if trace is not None:
-            trace.append({"draft_logits": dl, "verify_logits": vl})
-        S = S1 + acc + 1
-        x0 = t[acc].item()
+        S, x0, T, acc, rec = fulldraft_round(model, cache, S, x0, bd, mask_id, pos_offset, trace)
+        rounds.append(rec)
         out.extend(T)
     return out, rounds
 
