@@ -167,6 +167,7 @@ def main():
     if ar_tokens is not None:
         n = min(len(ar_tokens), len(spec_tokens))
         match = next((i for i in range(n) if ar_tokens[i] != spec_tokens[i]), n)
+        log(f"first ids: spec {spec_tokens[:8]} AR {ar_tokens[:8]}; identical prefix {match}")
 
     # ---- draft / verify halves (eager launches of the same kernels, graph-free timing) -------------------------
     # ---- planted acceptance ---------------------------------------------------------------------------------

@@ -16,17 +16,30 @@ SIGNATURES = {
     "gss_version": ([], ctypes.c_char_p),
     "gss_status_string": ([_i], ctypes.c_char_p),
     "gss_attn_workspace_size": ([_i, _i, _i, _i, _i, _i, _psz], _i),
+    "gss_attn_set_split_policy": ([_i, _i], _i),
     "gss_draft_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
     "gss_verify_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
     "gss_argmax_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_argmax_accept": ([_p, _i, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
     "gss_kv_commit_workspace_size": ([_i, _psz], _i),
     "gss_kv_commit": ([_p, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
+    "gss_gemm_set_policy": ([_i, _i], _i),
+    "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p], _i),
+    "gss_gemm_swiglu": ([_p, _i64, _p, _p, _i64, _p, _i, _i, _i, _p], _i),
+    "gss_gemm_rope_stage": ([_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
     "gss_rope_stage": ([_p, _i64, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "gss_rmsnorm": ([_p, _p, _p, _i, _i, _f, _p], _i),
     "gss_add_rmsnorm": ([_p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
     "gss_silu_mul": ([_p, _i64, _p, _i, _i, _p], _i),
 }
+
+
+
+class NormPrologue(ctypes.Structure):
+    """gss_norm_prologue (include/gss.h)."""
+    _fields_ = [("a", ctypes.c_void_p), ("h_in", ctypes.c_void_p), ("h_out", ctypes.c_void_p),
+                ("w_post", ctypes.c_void_p), ("w_next", ctypes.c_void_p), ("eps", ctypes.c_float)]
+
 
 _LIB = None
 

@@ -156,10 +156,14 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
   if (tid == 0) __hip_atomic_store(&p.counters[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Workspace layout: the per-sequence counters first (a fixed offset, whatever W and V are, so calls with different
+// window sizes can share one workspace), then the chunk winners' values and indices.
+constexpr size_t COUNTER_BYTES = 4096;  // up to 1024 sequences
+
 size_t ws_bytes(int bs, int W, int V) {
   const size_t nc = (static_cast<size_t>(V) + CHUNK - 1) / CHUNK;
   const size_t parts = static_cast<size_t>(bs) * W * nc;
-  return parts * (sizeof(float) + sizeof(int32_t)) + static_cast<size_t>(bs) * sizeof(uint32_t) + 64;
+  return COUNTER_BYTES + parts * (sizeof(float) + sizeof(int32_t));
 }
 
 }  // namespace
@@ -176,7 +180,7 @@ extern "C" int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, 
                                  int32_t* packed, void* workspace, size_t workspace_bytes, gss_stream_t stream) {
   if (!logits || !target || bs <= 0 || W <= 0 || V <= 0 || ld_row < V) return GSS_ERR_ARG;
   if (dtype != GSS_BF16 && dtype != GSS_F32) return GSS_ERR_ARG;
-  if (W > MAX_W) return GSS_ERR_UNSUPPORTED;
+  if (W > MAX_W || bs > static_cast<int>(COUNTER_BYTES / sizeof(uint32_t))) return GSS_ERR_UNSUPPORTED;
   if (!workspace || workspace_bytes < ws_bytes(bs, W, V)) return GSS_ERR_WORKSPACE;
   ArgParams p;
   p.logits = logits;
@@ -190,9 +194,9 @@ extern "C" int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, 
   p.next_x0 = next_x0;
   p.packed = packed;
   const size_t parts = static_cast<size_t>(bs) * W * p.n_chunks;
-  p.part_v = static_cast<float*>(workspace);
+  p.counters = static_cast<uint32_t*>(workspace);
+  p.part_v = reinterpret_cast<float*>(static_cast<char*>(workspace) + COUNTER_BYTES);
   p.part_i = reinterpret_cast<int32_t*>(p.part_v + parts);
-  p.counters = reinterpret_cast<uint32_t*>(p.part_i + parts);
   const dim3 grid(p.n_chunks, bs * W);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GSS_BF16)

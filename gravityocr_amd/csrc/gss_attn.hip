@@ -12,15 +12,18 @@
 //     moves between lanes.
 //   * K tiles live in LDS as [token][D] with an XOR swizzle of the 16-byte chunks (conflict-free 16-row reads);
 //     V pages are stored token-minor ([D][16] per page) in HBM, so the V^T operand is two 8-byte LDS reads.
-//   * Split-KV over prefix chunks (grid = splits x Hkv x bs) fills the chip at bs = 1; partial (m, l, O) go to the
-//     caller's workspace and a merge kernel combines them in split order (deterministic).
+//   * Keys are tiled by absolute position (window rows take the positions after the prefix), and split-KV
+//     partitions the tiles by capacity (grid = splits x Hkv x bs), so results do not depend on where a key comes
+//     from or on the prefix length: verify rows reproduce AR steps bit for bit. Partial (m, l, O) go to the
+//     caller's workspace and a merge kernel combines them in a fixed order.
 #include "gss_common.h"
 
 namespace {
 
 constexpr int PAGE = 16;
 constexpr int TILE = 64;  // KV tokens per LDS tile (4 pages)
-constexpr int MAX_WAVES = 16;
+constexpr int MAX_WAVES = 12;  // 768 threads: 3 waves per SIMD, 168 VGPRs per lane
+constexpr int MIN_WAVES = 4;   // extra waves only load tiles
 constexpr int MAX_NT = 24;  // query-row tiles per kv head (LDS: 32 KB K/V + MAX_NT * 16 * D * 2 B of Q)
 constexpr float LOG2E = 1.4426950408889634f;
 
@@ -35,7 +38,7 @@ struct AttnParams {
   uint16_t* out;
   float* ws_o;   // [bs, Hkv, n_split, R, D]
   float* ws_ml;  // [bs, Hkv, n_split, R, 2]
-  int pt_stride, prefix_extra, W, n_causal, Hq, Hkv, G, R, NT, n_split;
+  int pt_stride, prefix_extra, W, n_causal, Hq, Hkv, G, R, NT, n_split, tps;  // tps: 64-token tiles per split
   float scale_log2;
 };
 
@@ -45,7 +48,7 @@ GSS_DEV int k_lds_index(int tok, int chunk) {
   return (tok * (D / 8) + (chunk ^ (tok & (D / 8 - 1)))) * 8;
 }
 
-template <int D, int TPW>
+template <int D, int TPW, int CPT>
 __global__ void __launch_bounds__(64 * MAX_WAVES)
 window_attn_kernel(AttnParams p) {
   constexpr int KS = D / 32;   // MFMA K-steps over the head dim
@@ -151,69 +154,96 @@ window_attn_kernel(AttnParams p) {
     }
   };
 
-  // ---- prefix tiles of this split --------------------------------------------------------------------------
-  const int per = ((L + p.n_split - 1) / p.n_split + TILE - 1) / TILE * TILE;
-  const int beg = s * per;
-  const int end = min(L, beg + per);
+  // ---- the key sequence in absolute positions --------------------------------------------------------------
+  // Keys are positions 0 .. L+W-1: positions < L come from the pages, positions L .. L+W-1 are the window rows
+  // (staging). Tiles are the 64-position blocks [64t, 64t+64) and split s owns tiles [s*tps, (s+1)*tps) (tps depends
+  // only on the capacity max_kv_len). A query's visible keys therefore sit in the same tiles, accumulated in the same
+  // order, whether they are window rows or already in the pages: a verify row and the AR step of the same token
+  // compute bit-identical attention.
+  const int W = p.W, nc = p.n_causal;
+  const int n_tiles = (L + W + TILE - 1) / TILE;
+  const int t_beg = s * p.tps, t_end = min(n_tiles, t_beg + p.tps);
   const int32_t* pt = p.page_table + static_cast<int64_t>(b) * p.pt_stride;
   const int64_t head_stride = static_cast<int64_t>(PAGE) * D;  // elements per (page, kv head) block
+  const int64_t win_base = static_cast<int64_t>(b) * W * p.Hkv + kvh;  // row j of the window: (win_base + j*Hkv)*D
 
-  for (int tb = beg; tb < end; tb += TILE) {
-    const int nv = min(TILE, end - tb);
-    __syncthreads();
-    for (int c = tid; c < TILE * D / 8; c += nthr) {
-      const int j = c / (D / 8), part = c % (D / 8);
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (j < nv) {
-        const int page = pt[(tb + j) / PAGE];
-        v = *reinterpret_cast<const u32x4_t*>(
-            p.k_pages + (static_cast<int64_t>(page) * p.Hkv + kvh) * head_stride + ((tb + j) % PAGE) * D + part * 8);
-      }
-      *reinterpret_cast<u32x4_t*>(&lds_k[k_lds_index<D>(j, part)]) = v;
-    }
-    for (int c = tid; c < 4 * D * 2; c += nthr) {
-      const int pi = c / (D * 2), rem = c % (D * 2), d = rem >> 1, h = rem & 1;
-      const int t0 = pi * PAGE + h * 8;  // first token of this 8-token chunk (tile-relative)
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (t0 < nv) {
-        const int page = pt[(tb + pi * PAGE) / PAGE];
-        v = *reinterpret_cast<const u32x4_t*>(
-            p.v_pages + (static_cast<int64_t>(page) * p.Hkv + kvh) * head_stride + d * PAGE + h * 8);
-        const int keep = nv - t0;  // tokens of the chunk inside the valid range
-        if (keep < 8) {
+  // Tile loads go through registers: tile i+1's global loads are issued before tile i is computed, so HBM latency
+  // overlaps the MFMA work. Each thread owns chunks c = tid + k*nthr (k < CPT) of the K tile ([64 tok][D], 16 B
+  // each) and of the V tile ([4 pages][D][16 tok], 8 tokens of one dim each).
+  constexpr int NCH = TILE * D / 8;  // 16-byte chunks per K tile (and per V tile)
+  u32x4_t pk[CPT], pv[CPT];
+  auto load_tile = [&](int tb) {
+    int pg[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = (2 * e < keep) ? 0x0000ffffu : 0u, hi = (2 * e + 1 < keep) ? 0xffff0000u : 0u;
-            v[e] &= (lo | hi);
+    for (int i = 0; i < 4; ++i) pg[i] = (tb + i * PAGE < L) ? pt[tb / PAGE + i] : 0;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = tid + k * nthr;
+      pk[k] = u32x4_t{0u, 0u, 0u, 0u};
+      pv[k] = u32x4_t{0u, 0u, 0u, 0u};
+      if (c < NCH) {
+        const int j = c / (D / 8), part = c % (D / 8);
+        const int pos = tb + j;
+        if (pos < L)
+          pk[k] = *reinterpret_cast<const u32x4_t*>(
+              p.k_pages + (static_cast<int64_t>(pg[j / PAGE]) * p.Hkv + kvh) * head_stride + (j % PAGE) * D + part * 8);
+        else if (pos < L + W)
+          pk[k] = *reinterpret_cast<const u32x4_t*>(p.k_win + (win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D +
+                                                    part * 8);
+        const int pi = c / (D * 2), rem = c % (D * 2), d = rem >> 1, h = rem & 1;
+        const int t0 = tb + pi * PAGE + h * 8;  // absolute position of the chunk's first token
+        u32x4_t v = {0u, 0u, 0u, 0u};
+        if (t0 < L) {
+          v = *reinterpret_cast<const u32x4_t*>(
+              p.v_pages + (static_cast<int64_t>(pg[pi]) * p.Hkv + kvh) * head_stride + d * PAGE + h * 8);
+          const int keep = L - t0;  // tokens of the chunk inside the prefix
+          if (keep < 8) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t lo = (2 * e < keep) ? 0x0000ffffu : 0u, hi = (2 * e + 1 < keep) ? 0xffff0000u : 0u;
+              v[e] &= (lo | hi);
+            }
           }
         }
-      }
-      *reinterpret_cast<u32x4_t*>(&lds_v[(pi * D + d) * PAGE + h * 8]) = v;
-    }
-    __syncthreads();
-    compute_tile([nv](int, int tok) { return tok < nv; });
-  }
-
-  // ---- the window's own K/V: processed by the last split --------------------------------------------------
-  if (s == p.n_split - 1) {
-    __syncthreads();
-    const int W = p.W;
-    for (int c = tid; c < TILE * D / 8; c += nthr) {
-      const int j = c / (D / 8), part = c % (D / 8);
-      u32x4_t kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-      if (j < W) {
-        const int64_t off = ((static_cast<int64_t>(b) * W + j) * p.Hkv + kvh) * D + part * 8;
-        kv = *reinterpret_cast<const u32x4_t*>(p.k_win + off);
-        vv = *reinterpret_cast<const u32x4_t*>(p.v_win + off);
-      }
-      *reinterpret_cast<u32x4_t*>(&lds_k[k_lds_index<D>(j, part)]) = kv;
-      const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv);
+        if (t0 + 8 > L && t0 < L + W) {  // window rows inside this chunk (token-minor: one element per row)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) lds_v[((j / PAGE) * D + part * 8 + e) * PAGE + (j % PAGE)] = ve[e];
+          for (int e = 0; e < 8; ++e) {
+            const int pos = t0 + e;
+            if (pos >= L && pos < L + W) {
+              const uint32_t x = p.v_win[(win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D + d];
+              v[e >> 1] |= (e & 1) ? (x << 16) : x;
+            }
+          }
+        }
+        pv[k] = v;
+      }
     }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int c = tid + k * nthr;
+      if (c < NCH) {
+        *reinterpret_cast<u32x4_t*>(&lds_k[k_lds_index<D>(c / (D / 8), c % (D / 8))]) = pk[k];
+        const int pi = c / (D * 2), rem = c % (D * 2), d = rem >> 1, h = rem & 1;
+        *reinterpret_cast<u32x4_t*>(&lds_v[(pi * D + d) * PAGE + h * 8]) = pv[k];
+      }
+    }
+  };
+
+  if (t_beg < t_end) load_tile(t_beg * TILE);
+  for (int t = t_beg; t < t_end; ++t) {
+    const int tb = t * TILE;
+    __syncthreads();            // the previous tile's compute is done with LDS
+    store_tile();
     __syncthreads();
-    const int nc = p.n_causal;
-    compute_tile([W, nc](int roww, int tok) { return tok < W && (roww >= nc || tok <= roww); });
+    if (t + 1 < t_end) load_tile(tb + TILE);
+    compute_tile([tb, L, W, nc](int roww, int tok) {
+      const int pos = tb + tok;
+      if (pos < L) return true;
+      const int wj = pos - L;  // window row of this key
+      return wj < W && (roww >= nc || wj <= roww);
+    });
   }
 
   // ---- epilogue ------------------------------------------------------------------------------------------------
@@ -249,45 +279,58 @@ window_attn_kernel(AttnParams p) {
   }
 }
 
-// Combine the splits of each (sequence, kv head, row) in split order. One thread per 4 output elements.
+// Combine the splits of each (sequence, kv head, row). Block = one query row; thread (dg, sg) owns 4 head dims
+// and the splits sg, sg + SG, ...; the SG groups are combined through LDS in group order (deterministic).
 template <int D>
 __global__ void __launch_bounds__(256) window_attn_merge(AttnParams p) {
-  const int kvh = blockIdx.y, b = blockIdx.z;
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;  // (row, 4-element group)
-  if (idx >= p.R * (D / 4)) return;
-  const int n = idx / (D / 4), d0 = (idx % (D / 4)) * 4;
+  constexpr int DG = D / 4, SG = 256 / DG;
+  const int n = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int dg = threadIdx.x % DG, sg = threadIdx.x / DG;
   const int64_t hb = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.n_split;
-  float M = -INFINITY;
-  for (int s = 0; s < p.n_split; ++s) M = fmaxf(M, p.ws_ml[((hb + s) * p.R + n) * 2]);
-  float den = 0.f;
+  float M = -INFINITY, den = 0.f;
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < p.n_split; ++s) {
+  for (int s = sg; s < p.n_split; s += SG) {
     const int64_t r = (hb + s) * p.R + n;
     const float ms = p.ws_ml[r * 2];
     if (ms == -INFINITY) continue;
-    const float wgt = exp2f(ms - M);
-    den += p.ws_ml[r * 2 + 1] * wgt;
-    acc += *reinterpret_cast<const floatx4_t*>(p.ws_o + r * D + d0) * wgt;
+    const float ls = p.ws_ml[r * 2 + 1];
+    const floatx4_t os = *reinterpret_cast<const floatx4_t*>(p.ws_o + r * D + dg * 4);
+    const float Mn = fmaxf(M, ms);
+    const float a = exp2f(M - Mn), c = exp2f(ms - Mn);
+    den = den * a + ls * c;
+    acc = acc * a + os * c;
+    M = Mn;
   }
-  const float inv = 1.f / den;
+  __shared__ float sm[SG][DG], sd[SG][DG];
+  __shared__ floatx4_t sa[SG][DG];
+  sm[sg][dg] = M;
+  sd[sg][dg] = den;
+  sa[sg][dg] = acc;
+  __syncthreads();
+  if (sg != 0) return;
+  float Mt = sm[0][dg];
+  for (int g = 1; g < SG; ++g) Mt = fmaxf(Mt, sm[g][dg]);
+  float dt = 0.f;
+  floatx4_t at = {0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < SG; ++g) {
+    if (sm[g][dg] == -INFINITY) continue;
+    const float c = exp2f(sm[g][dg] - Mt);
+    dt += sd[g][dg] * c;
+    at += sa[g][dg] * c;
+  }
+  const float inv = 1.f / dt;
   const int w = n / p.G, gq = n % p.G;
   uint16_t* orow = p.out + ((static_cast<int64_t>(b) * p.W + w) * p.Hq + kvh * p.G + gq) * D;
-  *reinterpret_cast<u32x2_t*>(orow + d0) =
-      u32x2_t{pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+  *reinterpret_cast<u32x2_t*>(orow + dg * 4) =
+      u32x2_t{pack_bf16x2(at[0] * inv, at[1] * inv), pack_bf16x2(at[2] * inv, at[3] * inv)};
 }
 
-// Split count: enough (sequence, kv head, split) workgroups to cover the chip about twice, each split at least
-// GSS_MIN_TILES tiles of the longest prefix.
+// Split count: about target_wgs (sequence, kv head, split) workgroups, each split at least min_tiles 64-token
+// tiles of the longest prefix (gss_attn_set_split_policy).
+int g_target_wgs = 512, g_min_tiles = 2;
+
 int attn_splits(int bs, int Hkv, int max_kv_len) {
-  static int target_wgs = -1, min_tiles = -1;
-  if (target_wgs < 0) {
-    const char* e1 = getenv("GSS_ATTN_TARGET_WGS");
-    const char* e2 = getenv("GSS_ATTN_MIN_TILES");
-    target_wgs = e1 ? atoi(e1) : 512;
-    min_tiles = e2 ? atoi(e2) : 2;
-    if (target_wgs < 1) target_wgs = 512;
-    if (min_tiles < 1) min_tiles = 1;
-  }
+  const int target_wgs = g_target_wgs, min_tiles = g_min_tiles;
   const int tiles = (max(max_kv_len, 1) + TILE - 1) / TILE;
   int by_chip = (target_wgs + bs * Hkv - 1) / (bs * Hkv);
   int by_len = (tiles + min_tiles - 1) / min_tiles;
@@ -297,7 +340,7 @@ int attn_splits(int bs, int Hkv, int max_kv_len) {
 
 int choose_tpw(int NT, int* nw) {
   const int tpw = NT <= MAX_WAVES ? 1 : 2;
-  *nw = (NT + tpw - 1) / tpw;
+  *nw = max(MIN_WAVES, (NT + tpw - 1) / tpw);
   return tpw;
 }
 
@@ -311,27 +354,37 @@ int validate(int bs, int W, int Hq, int Hkv, int D, int page) {
   return GSS_OK;
 }
 
+template <int D, int TPW>
+void launch_kernel(const AttnParams& p, dim3 grid, int nw, size_t lds_q, hipStream_t st) {
+  constexpr int NCH = TILE * D / 8;
+  const int cpt = (NCH + 64 * nw - 1) / (64 * nw);
+  if (cpt <= 2)
+    hipLaunchKernelGGL((window_attn_kernel<D, TPW, 2>), grid, dim3(64 * nw), lds_q, st, p);
+  else
+    hipLaunchKernelGGL((window_attn_kernel<D, TPW, 4>), grid, dim3(64 * nw), lds_q, st, p);
+}
+
 template <int D>
 int launch_d(const AttnParams& p, int bs, int tpw, int nw, hipStream_t st) {
-  const dim3 grid(p.n_split, p.Hkv, bs), block(64 * nw);
+  const dim3 grid(p.n_split, p.Hkv, bs);
   const size_t lds_q = static_cast<size_t>(p.NT) * 16 * D * sizeof(uint16_t);
   static bool lds_attr_set = false;  // allow the dynamic Q tile beyond the default 64 KB (set once, before use)
   if (!lds_attr_set) {
     const int max_dyn = MAX_NT * 16 * D * static_cast<int>(sizeof(uint16_t));
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&window_attn_kernel<D, 1>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, max_dyn);
-    hipFuncSetAttribute(reinterpret_cast<const void*>(&window_attn_kernel<D, 2>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, max_dyn);
+    const void* fns[] = {reinterpret_cast<const void*>(&window_attn_kernel<D, 1, 2>),
+                         reinterpret_cast<const void*>(&window_attn_kernel<D, 1, 4>),
+                         reinterpret_cast<const void*>(&window_attn_kernel<D, 2, 2>),
+                         reinterpret_cast<const void*>(&window_attn_kernel<D, 2, 4>)};
+    for (const void* f : fns)
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, max_dyn) != hipSuccess)
+        return GSS_ERR_LAUNCH;
     lds_attr_set = true;
   }
   if (tpw == 1)
-    hipLaunchKernelGGL((window_attn_kernel<D, 1>), grid, block, lds_q, st, p);
+    launch_kernel<D, 1>(p, grid, nw, lds_q, st);
   else
-    hipLaunchKernelGGL((window_attn_kernel<D, 2>), grid, block, lds_q, st, p);
-  if (p.n_split > 1) {
-    const int n = p.R * (D / 4);
-    hipLaunchKernelGGL((window_attn_merge<D>), dim3((n + 255) / 256, p.Hkv, bs), dim3(256), 0, st, p);
-  }
+    launch_kernel<D, 2>(p, grid, nw, lds_q, st);
+  if (p.n_split > 1) hipLaunchKernelGGL((window_attn_merge<D>), dim3(p.R, p.Hkv, bs), dim3(256), 0, st, p);
   return gss_launch_status();
 }
 
@@ -362,6 +415,8 @@ int attn_entry(const void* q, const void* k_pages, const void* v_pages, const in
   p.R = p.G * W;
   p.NT = (p.R + 15) / 16;
   p.n_split = attn_splits(bs, Hkv, max_kv_len);
+  const int tiles_max = (max_kv_len + W + TILE - 1) / TILE;  // tiles of the longest key sequence
+  p.tps = (tiles_max + p.n_split - 1) / p.n_split;
   p.scale_log2 = scale * LOG2E;
   p.ws_o = nullptr;
   p.ws_ml = nullptr;
@@ -407,4 +462,11 @@ extern "C" int gss_verify_attn(const void* q, const void* k_pages, const void* v
   return attn_entry(q, k_pages, v_pages, page_table, pt_stride, prefix_len, prefix_extra, k_win, v_win, out, bs, W,
                     W, Hq, Hkv, D, page, scale, max_kv_len, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gss_attn_set_split_policy(int target_wgs, int min_tiles) {
+  if (target_wgs < 1 || min_tiles < 1) return GSS_ERR_ARG;
+  g_target_wgs = target_wgs;
+  g_min_tiles = min_tiles;
+  return GSS_OK;
 }

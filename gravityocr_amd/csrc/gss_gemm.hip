@@ -1,0 +1,427 @@
+// Skinny GEMM for the decode forwards: Y[M, N] = X[M, Kd] . W[N, Kd]^T with M <= 64 rows (bs * window),
+// bf16 operands, fp32 accumulation. Weight streaming is the whole cost (N*Kd*2 bytes per call), so the kernel is
+// built to keep many 16-byte weight loads in flight and to touch every weight byte exactly once.
+//
+// Layout on v_mfma_f32_16x16x32_bf16: A = 16 weight rows x 32 k (lane: row l%16, k 8*(l/16)..+7, one 16-byte
+// load), B = 32 k x 16 activation rows (lane: activation row l%16, same k), C = Y^T tile (lane: 4 consecutive
+// features of one activation row). A workgroup owns FT*16 output features; its waves split the k-steps into
+// contiguous ranges and reduce their partial tiles through LDS in wave order.
+//
+// Batch invariance: an output element is always the same sequence of MFMA k-steps and the same wave-order
+// reduction, whatever M is and wherever its row sits, so a row computed in a 17-row verify forward is bit-identical
+// to the same row computed alone (a 1-row AR step). Decode parity between speculative and AR decoding rests on it.
+//
+// Fused epilogues (the GEMM output is rounded to bf16 first, as a bf16 torch linear writes it):
+//   EPI_PLAIN   Y bf16 (or fp32) [M, ldy]
+//   EPI_ROPE    N = (Hq + 2 Hkv) * D q|k|v projection -> RoPE on q and k (interleaved pairs of the first rot_dim dims,
+//               position = seq_lens[b] + pos_delta[b] + w), written as q [bs, W, Hq, D] and window K/V [bs, W, Hkv, D]
+//   EPI_SWIGLU  N = 2F with gate/up rows interleaved (row 2i = gate_i, 2i+1 = up_i) -> act[M, F] = up * silu(gate)
+#include "gss_common.h"
+
+namespace {
+
+enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_SWIGLU = 2 };
+
+struct GemmParams {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* w;
+  int64_t ldw;
+  void* y;
+  int64_t ldy;
+  int M, N, Kd;
+  int out_f32;
+  // EPI_ROPE
+  const int32_t* seq_lens;
+  const int32_t* pos_delta;
+  const float* inv_freq;
+  int rot_dim, W, Hq, Hkv, D;
+  uint16_t* q_out;
+  uint16_t* k_out;
+  uint16_t* v_out;
+  // prologue (PRO_ADDNORM): x = rmsnorm(h') * w_next with h' = h_in + rmsnorm(a) * w_post (a == nullptr: h' = h_in);
+  // workgroup 0 stores h' to h_out (never h_in: other workgroups still read it)
+  const uint16_t* pa;
+  const uint16_t* h_in;
+  uint16_t* h_out;
+  const uint16_t* w_post;
+  const uint16_t* w_next;
+  float eps;
+};
+
+constexpr int MAX_NW = 12;  // waves per workgroup (768 threads: 168 VGPRs per lane)
+constexpr size_t MAX_LDS = 160 * 1024;  // LDS per workgroup on gfx950
+
+// Wave w owns the contiguous k-steps [w*ksw, (w+1)*ksw) and walks them in passes of UNR steps; every weight and
+// activation load of a pass is issued before the pass's first MFMA, so each wave keeps UNR*(FT+NT) 16-byte loads
+// in flight and a workgroup needs ceil(ksw / UNR) HBM round trips for its whole weight slice.
+enum { PRO_NONE = 0, PRO_ADDNORM = 1 };
+constexpr int XPAD = 8;  // bf16 elements of padding per LDS activation row (spreads rows over the LDS banks)
+
+// Prologue: the normalized activation rows x (bf16) go to LDS. One wavefront per row; lane l owns the E = Kd/64
+// consecutive elements [l*E, (l+1)*E); the arithmetic and rounding points are gss_add_rmsnorm's, so the fused and
+// unfused paths agree bit for bit.
+template <int E>
+GSS_DEV void addnorm_row(const GemmParams& p, int row, int lane, uint16_t* xs, bool store_h) {
+  constexpr int KD = 64 * E;
+  const int64_t off = static_cast<int64_t>(row) * KD + lane * E;
+  float hv[E], av[E], wn[E], wp[E];
+#pragma unroll
+  for (int c = 0; c < E / 8; ++c) {
+    const u32x4_t qh = *reinterpret_cast<const u32x4_t*>(p.h_in + off + c * 8);
+    const u32x4_t qn = *reinterpret_cast<const u32x4_t*>(p.w_next + lane * E + c * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hv[c * 8 + 2 * e] = __uint_as_float(qh[e] << 16);
+      hv[c * 8 + 2 * e + 1] = __uint_as_float(qh[e] & 0xffff0000u);
+      wn[c * 8 + 2 * e] = __uint_as_float(qn[e] << 16);
+      wn[c * 8 + 2 * e + 1] = __uint_as_float(qn[e] & 0xffff0000u);
+    }
+    if (p.pa != nullptr) {
+      const u32x4_t qa = *reinterpret_cast<const u32x4_t*>(p.pa + off + c * 8);
+      const u32x4_t qp = *reinterpret_cast<const u32x4_t*>(p.w_post + lane * E + c * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        av[c * 8 + 2 * e] = __uint_as_float(qa[e] << 16);
+        av[c * 8 + 2 * e + 1] = __uint_as_float(qa[e] & 0xffff0000u);
+        wp[c * 8 + 2 * e] = __uint_as_float(qp[e] << 16);
+        wp[c * 8 + 2 * e + 1] = __uint_as_float(qp[e] & 0xffff0000u);
+      }
+    }
+  }
+  if (p.pa != nullptr) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss += av[e] * av[e];
+    const float ra = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(KD) + p.eps);
+#pragma unroll
+    for (int e = 0; e < E; ++e) hv[e] = round_bf16(hv[e] + round_bf16(wp[e] * round_bf16(av[e] * ra)));
+  }
+  float sh = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) sh += hv[e] * hv[e];
+  const float rh = 1.f / sqrtf(wave_sum(sh) / static_cast<float>(KD) + p.eps);
+  uint16_t* xrow = xs + row * (KD + XPAD) + lane * E;
+#pragma unroll
+  for (int c = 0; c < E / 8; ++c) {
+    float xv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv[e] = wn[c * 8 + e] * round_bf16(hv[c * 8 + e] * rh);
+    *reinterpret_cast<u32x4_t*>(xrow + c * 8) = u32x4_t{pack_bf16x2(xv[0], xv[1]), pack_bf16x2(xv[2], xv[3]),
+                                                       pack_bf16x2(xv[4], xv[5]), pack_bf16x2(xv[6], xv[7])};
+    if (store_h)
+      *reinterpret_cast<u32x4_t*>(p.h_out + off + c * 8) =
+          u32x4_t{pack_bf16x2(hv[c * 8], hv[c * 8 + 1]), pack_bf16x2(hv[c * 8 + 2], hv[c * 8 + 3]),
+                  pack_bf16x2(hv[c * 8 + 4], hv[c * 8 + 5]), pack_bf16x2(hv[c * 8 + 6], hv[c * 8 + 7])};
+  }
+}
+
+template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8>
+__global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw) {
+  extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int f0 = blockIdx.x * FT * 16;
+  const int ksteps = p.Kd / 32;
+  const int s_beg = wv * ksw, s_end = min(ksteps, s_beg + ksw);
+
+  floatx4_t acc[FT][NT];
+#pragma unroll
+  for (int f = 0; f < FT; ++f)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint16_t* wrow[FT];
+#pragma unroll
+  for (int f = 0; f < FT; ++f) {
+    const int row = min(f0 + f * 16 + l16, p.N - 1);  // rows past N repeat the last (never stored)
+    wrow[f] = p.w + static_cast<int64_t>(row) * p.ldw + g4 * 8;
+  }
+  const uint16_t* xrow[NT];
+  bool xlive[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int r = n * 16 + l16;
+    xlive[n] = r < p.M;
+    xrow[n] = p.x + static_cast<int64_t>(xlive[n] ? r : 0) * p.ldx + g4 * 8;
+  }
+
+  uint16_t* xs = reinterpret_cast<uint16_t*>(red + NW * FT * NT * 64);
+  // PRO_ADDNORM runs exactly one pass on every wave (the prologue has a workgroup barrier)
+  const int sp_end = PRO == PRO_ADDNORM ? s_beg + 1 : s_end;
+  for (int sp = s_beg; sp < sp_end; sp += UNR) {
+    u32x4_t wa[UNR][FT];
+    u32x4_t xb[UNR][NT];
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      const int s = sp + u;
+      const bool on = s < s_end;
+#pragma unroll
+      for (int f = 0; f < FT; ++f)
+        wa[u][f] = on ? *reinterpret_cast<const u32x4_t*>(wrow[f] + s * 32) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    if constexpr (PRO == PRO_ADDNORM) {
+      // the weight loads above are in flight; build the normalized rows meanwhile (single pass: ksw <= UNR)
+      for (int r = wv; r < p.M; r += NW) addnorm_row<E>(p, r, lane, xs, blockIdx.x == 0 && p.h_out != nullptr);
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int s = sp + u;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          xb[u][n] = (s < s_end && xlive[n])
+                         ? *reinterpret_cast<const u32x4_t*>(xs + (n * 16 + l16) * (p.Kd + XPAD) + s * 32 + g4 * 8)
+                         : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const int s = sp + u;
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          xb[u][n] = (s < s_end && xlive[n]) ? *reinterpret_cast<const u32x4_t*>(xrow[n] + s * 32)
+                                             : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      if (sp + u < s_end) {
+#pragma unroll
+        for (int f = 0; f < FT; ++f)
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+            acc[f][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa[u][f]),
+                                                                __builtin_bit_cast(bf16x8_t, xb[u][n]), acc[f][n], 0,
+                                                                0, 0);
+      }
+    }
+  }
+
+  // ---- reduce the NW wave partials in wave order --------------------------------------------------------------
+#pragma unroll
+  for (int f = 0; f < FT; ++f)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) red[((wv * FT + f) * NT + n) * 64 + lane] = acc[f][n];
+  __syncthreads();
+  // wave v finishes tiles (f, n) with (f * NT + n) % NW == v
+#pragma unroll
+  for (int f = 0; f < FT; ++f)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      if ((f * NT + n) % NW != wv) continue;
+      floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
+      for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
+      const int row = n * 16 + l16;            // activation row
+      const int feat = f0 + f * 16 + g4 * 4;   // first of this lane's 4 consecutive output features
+      if (row >= p.M || feat >= p.N) continue;
+      float y0 = s[0], y1 = s[1], y2 = s[2], y3 = s[3];
+      if constexpr (EPI == EPI_PLAIN) {
+        if (p.out_f32) {
+          *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) = s;
+        } else {
+          *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) =
+              u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+        }
+      } else if constexpr (EPI == EPI_SWIGLU) {
+        // features (gate_i, up_i, gate_i+1, up_i+1), i = feat / 2
+        const float g0 = round_bf16(y0), u0 = round_bf16(y1), g1 = round_bf16(y2), u1 = round_bf16(y3);
+        const float s0 = round_bf16(g0 / (1.f + expf(-g0))), s1 = round_bf16(g1 / (1.f + expf(-g1)));
+        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat / 2) =
+            pack_bf16x2(u0 * s0, u1 * s1);
+      } else {  // EPI_ROPE
+        const int b = row / p.W, w = row % p.W;
+        const int head = feat / p.D, d = feat % p.D;  // 4 features never straddle a head (D % 16 == 0)
+        float o[4] = {round_bf16(y0), round_bf16(y1), round_bf16(y2), round_bf16(y3)};
+        if (head < p.Hq + p.Hkv) {
+          const int pos = p.seq_lens[b] + (p.pos_delta ? p.pos_delta[b] : 0) + w;
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            if (d + e < p.rot_dim) {
+              const float f = static_cast<float>(pos) * p.inv_freq[(d + e) >> 1];
+              const float c = round_bf16(cosf(f)), sn = round_bf16(sinf(f));
+              const float x0 = o[e], x1 = o[e + 1];
+              o[e] = round_bf16(round_bf16(x0 * c) - round_bf16(x1 * sn));
+              o[e + 1] = round_bf16(round_bf16(x1 * c) + round_bf16(x0 * sn));
+            }
+          }
+        }
+        uint16_t* dst;
+        if (head < p.Hq)
+          dst = p.q_out + (static_cast<int64_t>(row) * p.Hq + head) * p.D + d;
+        else if (head < p.Hq + p.Hkv)
+          dst = p.k_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq)) * p.D + d;
+        else
+          dst = p.v_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq - p.Hkv)) * p.D + d;
+        *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+      }
+    }
+}
+
+// Launch shape knobs (process-wide): the most waves per workgroup and the features per workgroup (0 = automatic).
+int g_max_nw = MAX_NW, g_ft = 0;
+
+template <int FT, int NT, int EPI, int PRO>
+int launch_ft_nt(const GemmParams& p, hipStream_t st) {
+  // k-steps per wave: the fewest that cover Kd with at most g_max_nw waves (rounded to a multiple of 4)
+  const int ksteps = p.Kd / 32;
+  int ksw = (ksteps + g_max_nw - 1) / g_max_nw;
+  ksw = (ksw + 3) / 4 * 4;
+  const int nw = (ksteps + ksw - 1) / ksw;
+  const dim3 grid((p.N + FT * 16 - 1) / (FT * 16)), block(64 * nw);
+  size_t lds = static_cast<size_t>(nw) * FT * NT * 64 * sizeof(floatx4_t);
+  if constexpr (PRO == PRO_ADDNORM) {
+    lds += static_cast<size_t>(p.M) * (p.Kd + XPAD) * sizeof(uint16_t);
+    if (ksw > 4) return GSS_ERR_UNSUPPORTED;  // one pass of 4 k-steps per wave: Kd <= 32 * 4 * MAX_NW
+    if (lds > MAX_LDS) return GSS_ERR_UNSUPPORTED;
+    switch (p.Kd / 64) {
+      case 4: hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO, 4>), grid, block, lds, st, p, ksw); break;
+      case 8: hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO, 8>), grid, block, lds, st, p, ksw); break;
+      case 16: hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO, 16>), grid, block, lds, st, p, ksw); break;
+      case 24: hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO, 24>), grid, block, lds, st, p, ksw); break;
+      default: return GSS_ERR_UNSUPPORTED;
+    }
+    return gss_launch_status();
+  } else {
+    if constexpr (FT + NT <= 3) {
+      if (ksw % 8 == 0) {
+        hipLaunchKernelGGL((gemm_kernel<FT, NT, 8, EPI>), grid, block, lds, st, p, ksw);
+        return gss_launch_status();
+      }
+    }
+    hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI>), grid, block, lds, st, p, ksw);
+    return gss_launch_status();
+  }
+}
+
+template <int EPI, int PRO>
+int launch_epi(const GemmParams& p, hipStream_t st) {
+  const int NT = (p.M + 15) / 16;
+  // 16 features per workgroup unless that makes more than ~8 workgroups per CU (the LM head)
+  if (g_ft == 1 || (g_ft == 0 && p.N / 16 <= 2048)) {
+    switch (NT) {
+      case 1: return launch_ft_nt<1, 1, EPI, PRO>(p, st);
+      case 2: return launch_ft_nt<1, 2, EPI, PRO>(p, st);
+      case 3: return launch_ft_nt<1, 3, EPI, PRO>(p, st);
+      default: return launch_ft_nt<1, 4, EPI, PRO>(p, st);
+    }
+  }
+  switch (NT) {
+    case 1: return launch_ft_nt<2, 1, EPI, PRO>(p, st);
+    case 2: return launch_ft_nt<2, 2, EPI, PRO>(p, st);
+    case 3: return launch_ft_nt<2, 3, EPI, PRO>(p, st);
+    default: return launch_ft_nt<2, 4, EPI, PRO>(p, st);
+  }
+}
+
+int gemm_entry(GemmParams& p, int epi, hipStream_t st) {
+  const bool pro = p.h_in != nullptr;
+  if ((!pro && !p.x) || !p.w || p.M <= 0 || p.N <= 0 || p.Kd <= 0) return GSS_ERR_ARG;
+  if (p.M > 64 || p.Kd % 32 != 0 || p.N % 16 != 0) return GSS_ERR_UNSUPPORTED;
+  if (p.ldw < p.Kd || (p.ldw % 8) || (!pro && (p.ldx < p.Kd || (p.ldx % 8)))) return GSS_ERR_ARG;
+  if ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.w)) & 15u) return GSS_ERR_ARG;
+  if (pro) {
+    if (!p.w_next || (p.pa && !p.w_post) || p.h_out == p.h_in) return GSS_ERR_ARG;
+    if (p.Kd % 512 != 0) return GSS_ERR_UNSUPPORTED;  // 8-element chunks per lane
+    if ((reinterpret_cast<uintptr_t>(p.h_in) | reinterpret_cast<uintptr_t>(p.pa) |
+         reinterpret_cast<uintptr_t>(p.h_out) | reinterpret_cast<uintptr_t>(p.w_next) |
+         reinterpret_cast<uintptr_t>(p.w_post)) & 15u)
+      return GSS_ERR_ARG;
+    switch (epi) {
+      case EPI_PLAIN: return launch_epi<EPI_PLAIN, PRO_ADDNORM>(p, st);
+      case EPI_SWIGLU: return launch_epi<EPI_SWIGLU, PRO_ADDNORM>(p, st);
+      default: return launch_epi<EPI_ROPE, PRO_ADDNORM>(p, st);
+    }
+  }
+  switch (epi) {
+    case EPI_PLAIN: return launch_epi<EPI_PLAIN, PRO_NONE>(p, st);
+    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU, PRO_NONE>(p, st);
+    default: return launch_epi<EPI_ROPE, PRO_NONE>(p, st);
+  }
+}
+
+// Fill the prologue fields of a GemmParams from the C descriptor (x comes from the prologue when h_in is set).
+void set_prologue(GemmParams& p, const gss_norm_prologue* pro) {
+  if (pro == nullptr) return;
+  p.pa = static_cast<const uint16_t*>(pro->a);
+  p.h_in = static_cast<const uint16_t*>(pro->h_in);
+  p.h_out = static_cast<uint16_t*>(pro->h_out);
+  p.w_post = static_cast<const uint16_t*>(pro->w_post);
+  p.w_next = static_cast<const uint16_t*>(pro->w_next);
+  p.eps = pro->eps;
+}
+
+}  // namespace
+
+extern "C" int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w, int64_t ldw, void* y,
+                        int64_t ldy, int M, int N, int Kd, int out_dtype, gss_stream_t stream) {
+  if (!y || ldy < N || (out_dtype != GSS_BF16 && out_dtype != GSS_F32)) return GSS_ERR_ARG;
+  if ((ldy % 4) || (reinterpret_cast<uintptr_t>(y) & 15u)) return GSS_ERR_ARG;
+  GemmParams p = {};
+  p.x = static_cast<const uint16_t*>(x);
+  p.ldx = ldx;
+  p.w = static_cast<const uint16_t*>(w);
+  p.ldw = ldw;
+  p.y = y;
+  p.ldy = ldy;
+  p.M = M;
+  p.N = N;
+  p.Kd = Kd;
+  p.out_f32 = out_dtype == GSS_F32;
+  set_prologue(p, pro);
+  return gemm_entry(p, EPI_PLAIN, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gss_gemm_swiglu(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_gu_interleaved,
+                               int64_t ldw, void* act, int M, int F, int Kd, gss_stream_t stream) {
+  if (!act || (reinterpret_cast<uintptr_t>(act) & 3u)) return GSS_ERR_ARG;
+  GemmParams p = {};
+  p.x = static_cast<const uint16_t*>(x);
+  p.ldx = ldx;
+  p.w = static_cast<const uint16_t*>(w_gu_interleaved);
+  p.ldw = ldw;
+  p.y = act;
+  p.ldy = F;
+  p.M = M;
+  p.N = 2 * F;
+  p.Kd = Kd;
+  set_prologue(p, pro);
+  return gemm_entry(p, EPI_SWIGLU, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_qkv,
+                                   int64_t ldw, const int32_t* seq_lens, const int32_t* pos_delta,
+                                   const float* inv_freq, int rot_dim, void* q, void* k_win, void* v_win, int bs,
+                                   int W, int Hq, int Hkv, int D, int Kd, gss_stream_t stream) {
+  if (!seq_lens || !inv_freq || !q || !k_win || !v_win || bs <= 0 || W <= 0) return GSS_ERR_ARG;
+  if (D % 16 != 0 || rot_dim < 0 || rot_dim > D || rot_dim % 2) return GSS_ERR_ARG;
+  GemmParams p = {};
+  p.x = static_cast<const uint16_t*>(x);
+  p.ldx = ldx;
+  p.w = static_cast<const uint16_t*>(w_qkv);
+  p.ldw = ldw;
+  p.y = nullptr;
+  p.M = bs * W;
+  p.N = (Hq + 2 * Hkv) * D;
+  p.Kd = Kd;
+  p.seq_lens = seq_lens;
+  p.pos_delta = pos_delta;
+  p.inv_freq = inv_freq;
+  p.rot_dim = rot_dim;
+  p.W = W;
+  p.Hq = Hq;
+  p.Hkv = Hkv;
+  p.D = D;
+  p.q_out = static_cast<uint16_t*>(q);
+  p.k_out = static_cast<uint16_t*>(k_win);
+  p.v_out = static_cast<uint16_t*>(v_win);
+  set_prologue(p, pro);
+  return gemm_entry(p, EPI_ROPE, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gss_gemm_set_policy(int max_waves, int features_per_wg) {
+  if (max_waves < 1 || max_waves > MAX_NW || (features_per_wg != 0 && features_per_wg != 16 && features_per_wg != 32))
+    return GSS_ERR_ARG;
+  g_max_nw = max_waves;
+  g_ft = features_per_wg / 16;
+  return GSS_OK;
+}

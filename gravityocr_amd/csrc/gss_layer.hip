@@ -49,45 +49,91 @@ __global__ void __launch_bounds__(256) rope_stage_kernel(const uint16_t* qkv, in
 
 // ---- RMSNorm -------------------------------------------------------------------------------------------------------
 // GlmOcrRMSNorm: y = x * 1/sqrt(mean(x^2) + eps) in fp32, rounded to bf16, then weight * y rounded to bf16.
-GSS_DEV float sum_squares_row(const uint16_t* x, int H, float* red) {
-  float ss = 0.f;
-  for (int j = threadIdx.x; j < H; j += blockDim.x) {
-    const float v = bf16_to_f32(x[j]);
-    ss += v * v;
+// One wavefront per row: lane l owns the E = H/64 consecutive elements [l*E, (l+1)*E) (loaded 16 bytes at a time
+// when E % 8 == 0), all loads are issued up front, and the row sums are xor-shuffle reductions (fixed order).
+constexpr int NORM_ROWS_PER_BLOCK = 4;
+constexpr int MAX_E = 32;  // H <= 2048
+
+template <int E>
+GSS_DEV void load_row(const uint16_t* src, float* v) {
+  if constexpr (E % 8 == 0) {
+#pragma unroll
+    for (int c = 0; c < E / 8; ++c) {
+      const u32x4_t q = *reinterpret_cast<const u32x4_t*>(src + c * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[c * 8 + 2 * e] = __uint_as_float(q[e] << 16);
+        v[c * 8 + 2 * e + 1] = __uint_as_float(q[e] & 0xffff0000u);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) v[e] = bf16_to_f32(src[e]);
   }
-  return block_sum(ss, red);
 }
 
-__global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const uint16_t* w, uint16_t* out, int H,
-                                                      float eps) {
-  __shared__ float red[4];
-  const uint16_t* xr = x + static_cast<int64_t>(blockIdx.x) * H;
-  uint16_t* orow = out + static_cast<int64_t>(blockIdx.x) * H;
-  const float r = 1.f / sqrtf(sum_squares_row(xr, H, red) / static_cast<float>(H) + eps);
-  for (int j = threadIdx.x; j < H; j += blockDim.x)
-    orow[j] = f32_to_bf16(bf16_to_f32(w[j]) * round_bf16(bf16_to_f32(xr[j]) * r));
+template <int E>
+GSS_DEV void store_row(uint16_t* dst, const float* v) {
+  if constexpr (E % 8 == 0) {
+#pragma unroll
+    for (int c = 0; c < E / 8; ++c)
+      *reinterpret_cast<u32x4_t*>(dst + c * 8) =
+          u32x4_t{pack_bf16x2(v[c * 8], v[c * 8 + 1]), pack_bf16x2(v[c * 8 + 2], v[c * 8 + 3]),
+                  pack_bf16x2(v[c * 8 + 4], v[c * 8 + 5]), pack_bf16x2(v[c * 8 + 6], v[c * 8 + 7])};
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) dst[e] = f32_to_bf16(v[e]);
+  }
 }
 
-// h = h + rmsnorm(a) * w_post ; x = rmsnorm(h) * w_next. One workgroup per row; the row of h stays in LDS.
-__global__ void __launch_bounds__(256) add_rmsnorm_kernel(const uint16_t* a, const uint16_t* w_post, uint16_t* h,
-                                                          const uint16_t* w_next, uint16_t* x, int H, float eps) {
-  extern __shared__ float hrow[];
-  __shared__ float red[4];
-  const int64_t off = static_cast<int64_t>(blockIdx.x) * H;
-  const float ra = 1.f / sqrtf(sum_squares_row(a + off, H, red) / static_cast<float>(H) + eps);
+template <int E>
+__global__ void __launch_bounds__(64 * NORM_ROWS_PER_BLOCK) rmsnorm_kernel(const uint16_t* x, const uint16_t* w,
+                                                                           uint16_t* out, int rows, float eps) {
+  constexpr int H = 64 * E;
+  const int row = blockIdx.x * NORM_ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float xv[E], wv[E];
+  load_row<E>(x + static_cast<int64_t>(row) * H + lane * E, xv);
+  load_row<E>(w + lane * E, wv);
   float ss = 0.f;
-  for (int j = threadIdx.x; j < H; j += blockDim.x) {
-    const float na = round_bf16(bf16_to_f32(w_post[j]) * round_bf16(bf16_to_f32(a[off + j]) * ra));
-    const float hn = round_bf16(bf16_to_f32(h[off + j]) + na);
-    hrow[j] = hn;
-    ss += hn * hn;
+#pragma unroll
+  for (int e = 0; e < E; ++e) ss += xv[e] * xv[e];
+  const float r = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int e = 0; e < E; ++e) xv[e] = wv[e] * round_bf16(xv[e] * r);
+  store_row<E>(out + static_cast<int64_t>(row) * H + lane * E, xv);
+}
+
+// h = h + rmsnorm(a) * w_post ; x = rmsnorm(h) * w_next (sandwich-norm residual, then the next norm)
+template <int E>
+__global__ void __launch_bounds__(64 * NORM_ROWS_PER_BLOCK) add_rmsnorm_kernel(const uint16_t* a,
+                                                                               const uint16_t* w_post, uint16_t* h,
+                                                                               const uint16_t* w_next, uint16_t* x,
+                                                                               int rows, float eps) {
+  constexpr int H = 64 * E;
+  const int row = blockIdx.x * NORM_ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int64_t off = static_cast<int64_t>(row) * H + lane * E;
+  float av[E], hv[E], wp[E], wn[E];
+  load_row<E>(a + off, av);
+  load_row<E>(h + off, hv);
+  load_row<E>(w_post + lane * E, wp);
+  load_row<E>(w_next + lane * E, wn);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) ss += av[e] * av[e];
+  const float ra = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(H) + eps);
+  float sh = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    hv[e] = round_bf16(hv[e] + round_bf16(wp[e] * round_bf16(av[e] * ra)));
+    sh += hv[e] * hv[e];
   }
-  const float rh = 1.f / sqrtf(block_sum(ss, red) / static_cast<float>(H) + eps);
-  for (int j = threadIdx.x; j < H; j += blockDim.x) {
-    const float hn = hrow[j];
-    h[off + j] = f32_to_bf16(hn);
-    x[off + j] = f32_to_bf16(bf16_to_f32(w_next[j]) * round_bf16(hn * rh));
-  }
+  const float rh = 1.f / sqrtf(wave_sum(sh) / static_cast<float>(H) + eps);
+  store_row<E>(h + off, hv);
+#pragma unroll
+  for (int e = 0; e < E; ++e) av[e] = wn[e] * round_bf16(hv[e] * rh);
+  store_row<E>(x + off, av);
 }
 
 // up * silu(gate): silu rounded to bf16 (torch's bf16 silu), then the product rounded.
@@ -117,23 +163,42 @@ extern "C" int gss_rope_stage(const void* qkv, int64_t ld_qkv, const int32_t* se
   return gss_launch_status();
 }
 
+#define GSS_NORM_CASES(X) X(1) X(2) X(4) X(6) X(8) X(12) X(16) X(24) X(32)
+
 extern "C" int gss_rmsnorm(const void* x, const void* w, void* out, int rows, int H, float eps,
                            gss_stream_t stream) {
   if (!x || !w || !out || rows <= 0 || H <= 0) return GSS_ERR_ARG;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out),
-                     H, eps);
+  if (H % 64 != 0 || H / 64 > MAX_E) return GSS_ERR_UNSUPPORTED;
+  const dim3 grid((rows + NORM_ROWS_PER_BLOCK - 1) / NORM_ROWS_PER_BLOCK), block(64 * NORM_ROWS_PER_BLOCK);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t *xs = static_cast<const uint16_t*>(x), *ws = static_cast<const uint16_t*>(w);
+  uint16_t* os = static_cast<uint16_t*>(out);
+  switch (H / 64) {
+#define X(E) \
+  case E: hipLaunchKernelGGL(rmsnorm_kernel<E>, grid, block, 0, st, xs, ws, os, rows, eps); break;
+    GSS_NORM_CASES(X)
+#undef X
+    default: return GSS_ERR_UNSUPPORTED;
+  }
   return gss_launch_status();
 }
 
 extern "C" int gss_add_rmsnorm(const void* a, const void* w_post, void* h, const void* w_next, void* x, int rows,
                                int H, float eps, gss_stream_t stream) {
   if (!a || !w_post || !h || !w_next || !x || rows <= 0 || H <= 0) return GSS_ERR_ARG;
-  if (H > 16384) return GSS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(rows), dim3(256), H * sizeof(float),
-                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(a),
-                     static_cast<const uint16_t*>(w_post), static_cast<uint16_t*>(h),
-                     static_cast<const uint16_t*>(w_next), static_cast<uint16_t*>(x), H, eps);
+  if (H % 64 != 0 || H / 64 > MAX_E) return GSS_ERR_UNSUPPORTED;
+  const dim3 grid((rows + NORM_ROWS_PER_BLOCK - 1) / NORM_ROWS_PER_BLOCK), block(64 * NORM_ROWS_PER_BLOCK);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t *as = static_cast<const uint16_t*>(a), *wp = static_cast<const uint16_t*>(w_post),
+                 *wn = static_cast<const uint16_t*>(w_next);
+  uint16_t *hs = static_cast<uint16_t*>(h), *xs = static_cast<uint16_t*>(x);
+  switch (H / 64) {
+#define X(E) \
+  case E: hipLaunchKernelGGL(add_rmsnorm_kernel<E>, grid, block, 0, st, as, wp, hs, wn, xs, rows, eps); break;
+    GSS_NORM_CASES(X)
+#undef X
+    default: return GSS_ERR_UNSUPPORTED;
+  }
   return gss_launch_status();
 }
 

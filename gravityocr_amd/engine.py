@@ -34,6 +34,7 @@ class _Bufs:
         rows = bs * W
         self.bs, self.W = bs, W
         self.h = torch.empty(rows, c.hidden, dtype=bf, device=dev)
+        self.h2 = torch.empty(rows, c.hidden, dtype=bf, device=dev)   # residual ping-pong for the fused norms
         self.x = torch.empty(rows, c.hidden, dtype=bf, device=dev)
         self.qkv = torch.empty(rows, c.qkv_dim, dtype=bf, device=dev)
         self.q = torch.empty(bs, W, c.n_heads, c.head_dim, dtype=bf, device=dev)
@@ -50,8 +51,11 @@ class GssEngine:
     """Weights, paged KV pool and kernels for up to ``max_bs`` sequences of up to ``max_len`` tokens each."""
 
     def __init__(self, cfg: GlmTextConfig, weights: Dict[str, torch.Tensor], *, max_bs: int, max_len: int,
-                 device="cuda", page_seed: int = 0, max_win: int = 48):
+                 device="cuda", page_seed: int = 0, max_win: int = 48, gemm: str = "gss"):
         self.cfg = cfg
+        # "gss": the batch-invariant skinny GEMMs (rows <= 64); "torch": hipBLASLt through torch.mm everywhere
+        self.gemm_impl = gemm
+        self.fuse_norm_rows = 4
         self.device = torch.device(device)
         self.max_bs, self.max_len, self.max_win = max_bs, max_len, max_win
         dev, bf = self.device, torch.bfloat16
@@ -63,7 +67,9 @@ class GssEngine:
         self.embed = up(weights["embed"])
         self.wqkv = [up(torch.cat([weights[f"{l}.wq"], weights[f"{l}.wk"], weights[f"{l}.wv"]], 0)) for l in range(L)]
         self.wo = [up(weights[f"{l}.wo"]) for l in range(L)]
-        self.wgu = [up(weights[f"{l}.w_gate_up"]) for l in range(L)]
+        # gate_up rows interleaved (2i = gate_i, 2i+1 = up_i) so one GEMM tile holds both halves of a SwiGLU unit
+        self.wgu = [up(weights[f"{l}.w_gate_up"].view(2, cfg.ffn, cfg.hidden).transpose(0, 1)
+                       .reshape(2 * cfg.ffn, cfg.hidden)) for l in range(L)]
         self.wdown = [up(weights[f"{l}.w_down"]) for l in range(L)]
         self.n_in = [up(weights[f"{l}.in_norm"]) for l in range(L)]
         self.n_psa = [up(weights[f"{l}.post_self_attn_norm"]) for l in range(L)]
@@ -115,22 +121,70 @@ class GssEngine:
             b.h.copy_(emb.view(bs * W, c.hidden))
         else:
             torch.index_select(self.embed, 0, ids.reshape(-1), out=b.h)
+        own = self.gemm_impl == "gss" and bs * W <= 64
+        # norms folded into the GEMM prologues pay off only for a few rows (each workgroup re-normalizes every row)
+        if own and bs * W <= self.fuse_norm_rows and c.hidden % 512 == 0 and c.hidden <= 1536:
+            return self._forward_fused(b, n_causal, sl, pt, pos_delta, mkl)
         K.rmsnorm(b.h, self.n_in[0], b.x, c.rms_eps)
         for l in range(c.n_layers):
-            torch.mm(b.x, self.wqkv[l].t(), out=b.qkv)
-            K.rope_stage(b.qkv, sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], pos_delta=pos_delta,
-                         rot_dim=c.rot_dim)
+            if own:
+                K.gemm_rope_stage(b.x, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l],
+                                  rot_dim=c.rot_dim, pos_delta=pos_delta)
+            else:
+                torch.mm(b.x, self.wqkv[l].t(), out=b.qkv)
+                K.rope_stage(b.qkv, sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], pos_delta=pos_delta,
+                             rot_dim=c.rot_dim)
             K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
                                n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
-            torch.mm(b.o.view(bs * W, -1), self.wo[l].t(), out=b.a)
+            if own:
+                K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a)
+            else:
+                torch.mm(b.o.view(bs * W, -1), self.wo[l].t(), out=b.a)
             K.add_rmsnorm(b.a, self.n_psa[l], b.h, self.n_pa[l], b.x, c.rms_eps)
-            torch.mm(b.x, self.wgu[l].t(), out=b.gu)
-            K.silu_mul(b.gu, b.act)
-            torch.mm(b.act, self.wdown[l].t(), out=b.a)
+            if own:
+                K.gemm_swiglu(b.x, self.wgu[l], b.act)
+                K.gemm(b.act, self.wdown[l], b.a)
+            else:
+                self._swiglu_torch(b.x, self.wgu[l], b.gu, b.act)
+                torch.mm(b.act, self.wdown[l].t(), out=b.a)
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
             K.add_rmsnorm(b.a, self.n_pm[l], b.h, nxt, b.x, c.rms_eps)
-        torch.mm(b.x, self.lm_head.t(), out=b.logits)
+        if own:
+            K.gemm(b.x, self.lm_head, b.logits)
+        else:
+            torch.mm(b.x, self.lm_head.t(), out=b.logits)
         return b.logits.view(bs, W, c.vocab)
+
+    def _forward_fused(self, b: _Bufs, n_causal, sl, pt, pos_delta, mkl) -> torch.Tensor:
+        """Decode forward with the sandwich norms folded into the GEMM prologues: per layer
+        [norm + qkv + RoPE], attention (+ split merge), o_proj, [norm + gate_up + SwiGLU], down."""
+        c = self.cfg
+        bs, W = b.bs, b.W
+        eps = c.rms_eps
+        h_a, h_b = b.h, b.h2
+        prev = None
+        for l in range(c.n_layers):
+            K.gemm_rope_stage(None, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], rot_dim=c.rot_dim,
+                              pos_delta=pos_delta,
+                              pro=dict(a=prev, h_in=h_a, h_out=h_b, w_post=self.n_pm[l - 1] if prev is not None else None,
+                                       w_next=self.n_in[l], eps=eps))
+            K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
+                               n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
+            K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a)
+            K.gemm_swiglu(None, self.wgu[l], b.act,
+                          pro=dict(a=b.a, h_in=h_b, h_out=h_a, w_post=self.n_psa[l], w_next=self.n_pa[l], eps=eps))
+            K.gemm(b.act, self.wdown[l], b.a)
+            prev = b.a
+        K.gemm(None, self.lm_head, b.logits,
+               pro=dict(a=b.a, h_in=h_a, h_out=None, w_post=self.n_pm[c.n_layers - 1], w_next=self.n_final, eps=eps))
+        return b.logits.view(bs, W, c.vocab)
+
+    @staticmethod
+    def _swiglu_torch(x, wgu_il, gu, act):
+        """hipBLASLt gate_up on the interleaved weight, then up * silu(gate) with torch's bf16 rounding."""
+        torch.mm(x, wgu_il.t(), out=gu)
+        g = gu.view(gu.shape[0], -1, 2)
+        torch.mul(g[..., 1], torch.nn.functional.silu(g[..., 0]), out=act)
 
     def commit(self, b: _Bufs, *, n_rows=None, n_add: int = 0, slots=None, seq_lens=None, page_table=None):
         bs = b.bs
@@ -177,9 +231,9 @@ class GssEngine:
                                    workspace=self.ws_attn)
             torch.mm(o.view(P, -1), self.wo[l].t(), out=a)
             K.add_rmsnorm(a, self.n_psa[l], h, self.n_pa[l], x, c.rms_eps)
-            gu = torch.mm(x, self.wgu[l].t())
+            gu = torch.empty(P, 2 * c.ffn, dtype=bf, device=dev)
             act = torch.empty(P, c.ffn, dtype=bf, device=dev)
-            K.silu_mul(gu, act)
+            self._swiglu_torch(x, self.wgu[l], gu, act)
             del gu
             torch.mm(act, self.wdown[l].t(), out=a)
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
@@ -222,6 +276,7 @@ class SelfSpecDecoder:
         self.verify_b = _Bufs(eng, bs, Kw)          # separate staging from the draft's
         self.ar_b = eng.bufs(bs, 1)
         self.ar_tgt = torch.zeros(bs, 1, **i32)
+        self.ar_ids = torch.zeros(bs, 1, **i32)
         self.ar_log = torch.zeros(max_rounds, bs, **i32)
         self.ar_ctr = torch.zeros(1, dtype=torch.int64, device=dev)
         self.g_round = None
@@ -247,7 +302,8 @@ class SelfSpecDecoder:
 
     def ar_step(self):
         e = self.eng
-        lg = e.forward(self.ar_b, ids=self.st.x0.view(self.bs, 1), n_causal=None)
+        self.ar_ids.copy_(self.st.x0.view(self.bs, 1))
+        lg = e.forward(self.ar_b, ids=self.ar_ids, n_causal=None)
         e.argmax(lg, self.ar_tgt)
         e.commit(self.ar_b, n_add=1)
         self.st.x0.copy_(self.ar_tgt[:, 0])

@@ -5,7 +5,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import check, lib
+from ._lib import NormPrologue, check, lib
 
 PAGE = 16
 
@@ -155,3 +155,78 @@ def add_rmsnorm(a, w_post, h, w_next, x, eps):
 def silu_mul(gu, out):
     rows, F = out.shape
     check(lib().gss_silu_mul(_ptr(gu), gu.stride(0), _ptr(out), rows, F, _stream()), "gss_silu_mul")
+
+
+def _gemm_args(x, w):
+    if w.dtype != torch.bfloat16 or not w.is_cuda or w.stride(1) != 1:
+        raise ValueError("gemm weights must be a bf16 GPU tensor with a dense last dimension")
+    if x is not None:
+        if x.dtype != torch.bfloat16 or not x.is_cuda or x.stride(1) != 1:
+            raise ValueError("gemm activations must be a bf16 GPU tensor with a dense last dimension")
+        if x.shape[1] != w.shape[1]:
+            raise ValueError(f"gemm inner dims differ: {tuple(x.shape)} x {tuple(w.shape)}^T")
+
+
+def _prologue(pro, M, Kd):
+    """pro = dict(h_in=..., w_next=..., eps=..., a=None, w_post=None, h_out=None) -> (NormPrologue or None)."""
+    if pro is None:
+        return None
+    for k in ("h_in", "a", "h_out"):
+        t = pro.get(k)
+        if t is not None:
+            _need(t, torch.bfloat16, f"prologue {k}", (M, Kd))
+    for k in ("w_next", "w_post"):
+        t = pro.get(k)
+        if t is not None:
+            _need(t, torch.bfloat16, f"prologue {k}", (Kd,))
+    return NormPrologue(_ptr(pro.get("a")).value, _ptr(pro["h_in"]).value, _ptr(pro.get("h_out")).value,
+                        _ptr(pro.get("w_post")).value, _ptr(pro["w_next"]).value, float(pro["eps"]))
+
+
+def _rows(x, pro):
+    return (x.shape[0], x.stride(0)) if x is not None else (pro["h_in"].shape[0], 0)
+
+
+def gemm(x, w, y, pro=None):
+    """y[M, N] = x[M, Kd] @ w[N, Kd]^T (bf16 or fp32 y), M <= 64, batch invariant. With ``pro`` (a dict of the
+    gss_norm_prologue fields) x is rmsnorm(h_in + rmsnorm(a) * w_post) * w_next, built inside the kernel."""
+    _gemm_args(x, w)
+    Kd, N = w.shape[1], w.shape[0]
+    M, ldx = _rows(x, pro)
+    if y.shape[0] != M or y.shape[1] < N or y.stride(1) != 1:
+        raise ValueError("gemm output shape")
+    dt = {torch.bfloat16: 0, torch.float32: 1}[y.dtype]
+    pr = _prologue(pro, M, Kd)
+    check(lib().gss_gemm(_ptr(x), ldx, None if pr is None else ctypes.byref(pr), _ptr(w), w.stride(0), _ptr(y),
+                         y.stride(0), M, N, Kd, dt, _stream()), "gss_gemm")
+
+
+def gemm_swiglu(x, w_gu_il, act, pro=None):
+    """act[M, F] = up * silu(gate) of x @ w_gu_il^T, w_gu_il [2F, Kd] with gate/up rows interleaved."""
+    _gemm_args(x, w_gu_il)
+    Kd, F = w_gu_il.shape[1], w_gu_il.shape[0] // 2
+    M, ldx = _rows(x, pro)
+    _need(act, torch.bfloat16, "act", (M, F))
+    pr = _prologue(pro, M, Kd)
+    check(lib().gss_gemm_swiglu(_ptr(x), ldx, None if pr is None else ctypes.byref(pr), _ptr(w_gu_il),
+                                w_gu_il.stride(0), _ptr(act), M, F, Kd, _stream()), "gss_gemm_swiglu")
+
+
+def gemm_rope_stage(x, w_qkv, seq_lens, inv_freq, q, k_win, v_win, *, rot_dim, pos_delta=None, pro=None):
+    """q|k|v projection with RoPE and window staging fused: q [bs, W, Hq, D], k_win/v_win [bs, W, Hkv, D]."""
+    _gemm_args(x, w_qkv)
+    bs, W, Hq, D = q.shape
+    Hkv = k_win.shape[2]
+    Kd = w_qkv.shape[1]
+    M, ldx = _rows(x, pro)
+    if M != bs * W or w_qkv.shape[0] != (Hq + 2 * Hkv) * D:
+        raise ValueError("gemm_rope_stage shapes")
+    _need(seq_lens, torch.int32, "seq_lens", (bs,))
+    _need(q, torch.bfloat16, "q")
+    _need(k_win, torch.bfloat16, "k_win", (bs, W, Hkv, D))
+    _need(v_win, torch.bfloat16, "v_win", (bs, W, Hkv, D))
+    pr = _prologue(pro, M, Kd)
+    check(lib().gss_gemm_rope_stage(_ptr(x), ldx, None if pr is None else ctypes.byref(pr), _ptr(w_qkv),
+                                    w_qkv.stride(0), _ptr(seq_lens), _ptr(pos_delta), _ptr(inv_freq), rot_dim,
+                                    _ptr(q), _ptr(k_win), _ptr(v_win), bs, W, Hq, Hkv, D, Kd, _stream()),
+          "gss_gemm_rope_stage")

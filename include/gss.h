@@ -59,6 +59,10 @@ const char* gss_status_string(int status);
  */
 int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes);
 
+/* Split-KV policy of both attention kernels: about target_wgs (sequence, kv head, split) workgroups per launch, each
+ * split covering at least min_tiles 64-token tiles (defaults 512 and 2). Process-wide; set before sizing workspaces. */
+int gss_attn_set_split_policy(int target_wgs, int min_tiles);
+
 int gss_draft_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int pt_stride,
                    const int32_t* prefix_len, int prefix_extra, const void* k_win, const void* v_win, void* out,
                    int bs, int W, int n_causal, int Hq, int Hkv, int D, int page, float scale, int max_kv_len,
@@ -80,7 +84,8 @@ int gss_verify_attn(const void* q, const void* k_pages, const void* v_pages, con
  *   next_x0[b]    = target[b, accept_len[b]]              (the correction, or the bonus when all W-1 matched)
  *   packed[b]     = (window[b,0], accept_len[b], target[b,0..W-1] with entries past accept_len zeroed)
  *                   the row layout of _ss_commit_kernel's readback (selfspec_fast_commit.py:125-138); may be NULL.
- * Workspace: gss_argmax_workspace_size bytes, zeroed once after allocation.
+ * Workspace: gss_argmax_workspace_size bytes, zeroed once after allocation. Its first 4 KiB are per-sequence
+ * counters at a fixed offset, so one workspace serves calls with different W (sized for the largest).
  */
 int gss_argmax_workspace_size(int bs, int W, int V, size_t* bytes);
 
@@ -104,6 +109,45 @@ int gss_kv_commit(const void* k_win, const void* v_win, int64_t win_layer_stride
                   int64_t page_layer_stride, const int32_t* page_table, int pt_stride, int32_t* seq_lens,
                   const int32_t* n_rows, int n_add, int32_t* slots, int bs, int W, int n_layers, int Hkv, int D,
                   int page, void* workspace, size_t workspace_bytes, gss_stream_t stream);
+
+/* ---------------------------------------------------------------- skinny GEMMs (decode projections) ----------
+ * The dense projections of the decoder layer and the LM head (transformers GlmOcrTextAttention q/k/v/o_proj,
+ * GlmOcrTextMLP gate_up/down_proj and lm_head, which the reference runs as torch linears through
+ * src/fast_sampling.py:89-102). Y[M, N] = X[M, Kd] . W[N, Kd]^T, bf16 operands (row strides in elements, 16-byte
+ * aligned), fp32 accumulation, M <= 64, Kd % 32 == 0, N % 16 == 0. A row's result does not depend on M or on the
+ * row's position (batch invariant), so speculative verify rows reproduce AR rows bit for bit.
+ * gss_gemm: Y bf16 or fp32. gss_gemm_swiglu: W = gate_up with gate/up rows interleaved (2i = gate_i, 2i+1 = up_i),
+ * act[M, F] = up * silu(gate). gss_gemm_rope_stage: W = [Wq; Wk; Wv], output q [bs, W, Hq, D] rotated,
+ * window K/V [bs, W, Hkv, D] with K rotated (positions as gss_rope_stage with pos_offset 0).
+ */
+/* Optional fused prologue of the three GEMMs below (the GLM sandwich norm between sub-layers, GlmOcrTextDecoderLayer):
+ *   h' = h_in + rmsnorm(a) * w_post   (a == NULL: h' = h_in),   x = rmsnorm(h') * w_next,   Y = x . W^T
+ * with gss_add_rmsnorm's arithmetic (bit-identical to the unfused pair). Workgroup 0 stores h' to h_out (NULL: not
+ * stored; must not alias h_in). Rows are Kd wide; needs Kd % 512 == 0 and Kd <= 1536. With pro == NULL the GEMM reads
+ * x/ldx directly. */
+typedef struct gss_norm_prologue {
+  const void* a;      /* bf16 [M, Kd] or NULL */
+  const void* h_in;   /* bf16 [M, Kd] residual stream */
+  void* h_out;        /* bf16 [M, Kd] or NULL */
+  const void* w_post; /* bf16 [Kd], used with a */
+  const void* w_next; /* bf16 [Kd] */
+  float eps;
+} gss_norm_prologue;
+
+/* Launch-shape policy of the three GEMMs (process-wide): at most max_waves (1..12) waves per workgroup splitting
+ * Kd, and features_per_wg output features per workgroup (16 or 32; 0 = 16 unless N > 32768). */
+int gss_gemm_set_policy(int max_waves, int features_per_wg);
+
+int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w, int64_t ldw, void* y,
+             int64_t ldy, int M, int N, int Kd, int out_dtype, gss_stream_t stream);
+
+int gss_gemm_swiglu(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_gu_interleaved,
+                    int64_t ldw, void* act, int M, int F, int Kd, gss_stream_t stream);
+
+int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_qkv, int64_t ldw,
+                        const int32_t* seq_lens, const int32_t* pos_delta, const float* inv_freq, int rot_dim,
+                        void* q, void* k_win, void* v_win, int bs, int W, int Hq, int Hkv, int D, int Kd,
+                        gss_stream_t stream);
 
 /* ---------------------------------------------------------------- decoder-layer helpers -------------------------
  * Fused elementwise pieces of the GLM text decoder layer (transformers GlmOcrTextDecoderLayer, which the reference

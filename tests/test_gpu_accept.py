@@ -112,3 +112,17 @@ def test_full_accept_and_no_accept(cuda):
     t, acc, nx, packed = run(cuda, logits, window)
     assert list(acc) == [W - 1, 0]
     assert nx[0] == tgt[0, W - 1] and nx[1] == tgt[1, 0]
+
+
+def test_workspace_shared_across_window_sizes(cuda):
+    """Regression: one workspace serving W = 17 and W = 1 calls in turn (the round's argmax and the AR step's)."""
+    from gravityocr_amd.kernels import argmax_accept, argmax_workspace_bytes
+    V = 59392
+    ws = torch.zeros(argmax_workspace_bytes(1, 17, V), dtype=torch.uint8, device=cuda)
+    for it in range(3):
+        for W in (17, 1, 9, 1):
+            logits, window, tgt = make_case(1, W, V, seed=50 + 10 * it + W)
+            t = torch.full((1, W), -7, dtype=torch.int32, device=cuda)
+            argmax_accept(logits.to(cuda), t, ws)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(t.cpu().numpy(), tgt)
