@@ -28,6 +28,7 @@ SIGNATURES = {
     "gss_gemm_swiglu": ([_p, _i64, _p, _p, _i64, _p, _i, _i, _i, _p], _i),
     "gss_gemm_rope_stage": ([_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
     "gss_rope_stage": ([_p, _i64, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
+    "gss_rope_stage_mrope": ([_p, _i64, _p, _i, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _p], _i),
     "gss_rmsnorm": ([_p, _p, _p, _i, _i, _f, _p], _i),
     "gss_add_rmsnorm": ([_p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
     "gss_silu_mul": ([_p, _i64, _p, _i, _i, _p], _i),

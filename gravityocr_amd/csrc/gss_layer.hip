@@ -12,12 +12,15 @@ namespace {
 // bf16 (modeling_glm_ocr.py:129-173): out0 = x0*c - x1*s, out1 = x1*c + x0*s, each product and sum rounded to bf16.
 __global__ void __launch_bounds__(256) rope_stage_kernel(const uint16_t* qkv, int64_t ld_qkv, const int32_t* seq_lens,
                                                          const int32_t* pos_delta, int pos_offset,
+                                                         const int32_t* pos3, int sec0, int sec01,
                                                          const float* inv_freq, int rot_dim, uint16_t* q,
                                                          uint16_t* k_win, uint16_t* v_win, int W, int Hq, int Hkv,
                                                          int D) {
   const int row = blockIdx.x;  // b * W + w
   const int b = row / W, w = row % W;
-  const int pos = seq_lens[b] + (pos_delta ? pos_delta[b] : 0) + pos_offset + w;
+  // M-RoPE: with an explicit (t, h, w) position table, frequency i takes component 0 below sec0, 1 below sec01, else 2
+  const int* p3 = pos3 ? pos3 + static_cast<int64_t>(row) * 3 : nullptr;
+  const int pos = p3 ? 0 : seq_lens[b] + (pos_delta ? pos_delta[b] : 0) + pos_offset + w;
   const uint16_t* src = qkv + static_cast<int64_t>(row) * ld_qkv;
   const int half = D / 2;
   const int n_rot_heads = Hq + Hkv;
@@ -34,7 +37,8 @@ __global__ void __launch_bounds__(256) rope_stage_kernel(const uint16_t* qkv, in
     uint32_t y2 = x2;
     if (d0 < rot_dim) {
       const float x0 = __uint_as_float(x2 << 16), x1 = __uint_as_float(x2 & 0xffff0000u);
-      const float f = static_cast<float>(pos) * inv_freq[i];
+      const int pi = p3 ? p3[i < sec0 ? 0 : (i < sec01 ? 1 : 2)] : pos;
+      const float f = static_cast<float>(pi) * inv_freq[i];
       const float c = round_bf16(cosf(f)), s = round_bf16(sinf(f));
       const float y0 = round_bf16(round_bf16(x0 * c) - round_bf16(x1 * s));
       const float y1 = round_bf16(round_bf16(x1 * c) + round_bf16(x0 * s));
@@ -157,9 +161,24 @@ extern "C" int gss_rope_stage(const void* qkv, int64_t ld_qkv, const int32_t* se
   if (rot_dim < 0 || rot_dim > D || rot_dim % 2 != 0 || ld_qkv < static_cast<int64_t>(Hq + 2 * Hkv) * D)
     return GSS_ERR_ARG;
   hipLaunchKernelGGL(rope_stage_kernel, dim3(bs * W), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(qkv), ld_qkv, seq_lens, pos_delta, pos_offset, inv_freq, rot_dim,
-                     static_cast<uint16_t*>(q), static_cast<uint16_t*>(k_win), static_cast<uint16_t*>(v_win), W, Hq,
-                     Hkv, D);
+                     static_cast<const uint16_t*>(qkv), ld_qkv, seq_lens, pos_delta, pos_offset, nullptr, 0, 0,
+                     inv_freq, rot_dim, static_cast<uint16_t*>(q), static_cast<uint16_t*>(k_win),
+                     static_cast<uint16_t*>(v_win), W, Hq, Hkv, D);
+  return gss_launch_status();
+}
+
+extern "C" int gss_rope_stage_mrope(const void* qkv, int64_t ld_qkv, const int32_t* positions, int sec_t, int sec_h,
+                                    const float* inv_freq, int rot_dim, void* q, void* k_win, void* v_win, int rows,
+                                    int Hq, int Hkv, int D, gss_stream_t stream) {
+  if (!qkv || !positions || !inv_freq || !q || !k_win || !v_win) return GSS_ERR_ARG;
+  if (rows <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || D % 2 != 0 || sec_t < 0 || sec_h < 0) return GSS_ERR_ARG;
+  if (rot_dim < 0 || rot_dim > D || rot_dim % 2 != 0 || ld_qkv < static_cast<int64_t>(Hq + 2 * Hkv) * D)
+    return GSS_ERR_ARG;
+  // one sequence of `rows` window rows; seq_lens is not read when the position table is given
+  hipLaunchKernelGGL(rope_stage_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(qkv), ld_qkv, nullptr, nullptr, 0, positions, sec_t,
+                     sec_t + sec_h, inv_freq, rot_dim, static_cast<uint16_t*>(q), static_cast<uint16_t*>(k_win),
+                     static_cast<uint16_t*>(v_win), rows, Hq, Hkv, D);
   return gss_launch_status();
 }
 

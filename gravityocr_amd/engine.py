@@ -197,14 +197,19 @@ class GssEngine:
         K.argmax_accept(logits, target, self.ws_arg, **kw)
 
     # ------------------------------------------------------------------------------------------ prefill ---------
-    def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 48, pos_delta: Optional[torch.Tensor] = None):
+    def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 48, pos_delta: Optional[torch.Tensor] = None,
+                positions: Optional[torch.Tensor] = None, logits_rows: Optional[Tuple[int, int]] = None):
         """Causal prefill of one sequence slot from its prompt embeddings [P, H]: whole-prompt GEMMs, attention in
         causal chunks of ``chunk`` rows through the verify kernel (prefix from the pages, chunk as the window),
-        K/V committed layer by layer. Returns the logits of the last prompt row [V] (bf16)."""
+        K/V committed layer by layer. Row j sits at position j (+ pos_delta), or at the M-RoPE positions
+        ``positions`` int32 [P, 3] (t, h, w) when given. Returns the logits of the last prompt row [V] (bf16), or of
+        rows [r0, r1) as [r1 - r0, V] when ``logits_rows`` = (r0, r1)."""
         c, dev, bf = self.cfg, self.device, torch.bfloat16
         P = emb.shape[0]
         if P > self.max_len:
             raise ValueError("prompt longer than the engine capacity")
+        if positions is not None and tuple(positions.shape) != (P, 3):
+            raise ValueError("positions must be [P, 3]")
         pt = self.page_table[slot:slot + 1]
         h = emb.to(device=dev, dtype=bf).contiguous().clone()
         x = torch.empty_like(h)
@@ -217,10 +222,15 @@ class GssEngine:
         zero = torch.zeros(1, dtype=torch.int32, device=dev)
         starts = torch.arange(0, P, chunk, dtype=torch.int32, device=dev)
         lens = torch.zeros(1, dtype=torch.int32, device=dev)
+        pos3 = None if positions is None else positions.to(device=dev, dtype=torch.int32).contiguous()
         K.rmsnorm(h, self.n_in[0], x, c.rms_eps)
         for l in range(c.n_layers):
             torch.mm(x, self.wqkv[l].t(), out=qkv)
-            K.rope_stage(qkv, zero, self.inv_freq, q, kw[0], vw[0], pos_delta=pos_delta, rot_dim=c.rot_dim)
+            if positions is not None:
+                K.rope_stage_mrope(qkv, pos3, self.inv_freq, q[0], kw[0, 0], vw[0, 0], sections=c.mrope_section,
+                                   rot_dim=c.rot_dim)
+            else:
+                K.rope_stage(qkv, zero, self.inv_freq, q, kw[0], vw[0], pos_delta=pos_delta, rot_dim=c.rot_dim)
             lens.zero_()
             K.kv_commit(kw, vw, self.k_pages[l:l + 1], self.v_pages[l:l + 1], pt, lens, self.ws_commit, n_add=P)
             for i, s0 in enumerate(range(0, P, chunk)):
@@ -239,6 +249,9 @@ class GssEngine:
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
             K.add_rmsnorm(a, self.n_pm[l], h, nxt, x, c.rms_eps)
         self.seq_lens[slot:slot + 1].fill_(P)
+        if logits_rows is not None:
+            r0, r1 = logits_rows
+            return x[r0:r1] @ self.lm_head.t()
         return (x[P - 1:P] @ self.lm_head.t())[0]
 
 
@@ -274,6 +287,12 @@ class SelfSpecDecoder:
                              ctr=torch.zeros(1, dtype=torch.int64, device=dev))
         self.draft_b = eng.bufs(bs, Kw)
         self.verify_b = _Bufs(eng, bs, Kw)          # separate staging from the draft's
+        self.r0_b = None                            # round 0's [MASK x B] draft window, made on first use
+        self.r0_ids = torch.full((bs, bd), mask_id, **i32)
+        self.r0_am = torch.zeros(bs, bd, **i32)
+        self.pos_delta = torch.zeros(bs, **i32)     # position - cache index of every response row (M-RoPE delta)
+        self.log_am = torch.zeros(max_rounds, bs, Kw, **i32)    # every round's verify window (the draft)
+        self.log_tgt = torch.zeros(max_rounds, bs, Kw, **i32)   # every round's verify argmax
         self.ar_b = eng.bufs(bs, 1)
         self.ar_tgt = torch.zeros(bs, 1, **i32)
         self.ar_ids = torch.zeros(bs, 1, **i32)
@@ -288,22 +307,43 @@ class SelfSpecDecoder:
         verify forward and may rewrite the verify window ``st.am[:, 1:]`` (the planted-acceptance measurement)."""
         e, s = self.eng, self.st
         s.win[:, 0].copy_(s.x0)
-        lg = e.forward(self.draft_b, ids=s.win, n_causal=1)
+        lg = e.forward(self.draft_b, ids=s.win, n_causal=1, pos_delta=self.pos_delta)
         e.argmax(lg, s.am)                                                  # a0, d_1..d_B
         e.commit(self.draft_b, n_add=1)                                     # x0's K/V (causal row 0): S += 1
         if after_draft is not None:
             after_draft()
-        lg = e.forward(self.verify_b, ids=s.am, n_causal=None)
+        self._verify()
+
+    def round0(self):
+        """The first round of the reference's cached decode (src/fast_sampling.py:519-560 with pending = None): the
+        prefill's argmax a0 (in st.x0, no K/V) seeds block[0]; the draft window is [MASK x B] at the next B
+        positions, all rows bidirectional, and its rows 0..B-1 give d_1..d_B; the verify half of the round then runs
+        on [a0, d_1..d_B] at positions S.. exactly as in every later round."""
+        e, s = self.eng, self.st
+        if self.r0_b is None:
+            self.r0_b = e.bufs(self.bs, self.bd)
+        lg = e.forward(self.r0_b, ids=self.r0_ids, n_causal=0, pos_delta=self.pos_delta)
+        e.argmax(lg, self.r0_am)
+        s.am[:, 0].copy_(s.x0)
+        s.am[:, 1:].copy_(self.r0_am)
+        self._verify()
+
+    def _verify(self):
+        e, s = self.eng, self.st
+        lg = e.forward(self.verify_b, ids=s.am, n_causal=None, pos_delta=self.pos_delta)
         e.argmax(lg, s.tgt, window=s.am, accept_len=s.acc, next_x0=s.x0, packed=s.packed)
         e.commit(self.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)       # a0, d_1..d_acc: S += acc + 1
         # the log index is clamped on the device, so rounds beyond the log's capacity rewrite its last row
-        s.log.index_copy_(0, s.ctr.clamp(max=s.log.shape[0] - 1), s.packed.unsqueeze(0))
+        li = s.ctr.clamp(max=s.log.shape[0] - 1)
+        s.log.index_copy_(0, li, s.packed.unsqueeze(0))
+        self.log_am.index_copy_(0, li, s.am.unsqueeze(0))
+        self.log_tgt.index_copy_(0, li, s.tgt.unsqueeze(0))
         s.ctr.add_(1)
 
     def ar_step(self):
         e = self.eng
         self.ar_ids.copy_(self.st.x0.view(self.bs, 1))
-        lg = e.forward(self.ar_b, ids=self.ar_ids, n_causal=None)
+        lg = e.forward(self.ar_b, ids=self.ar_ids, n_causal=None, pos_delta=self.pos_delta)
         e.argmax(lg, self.ar_tgt)
         e.commit(self.ar_b, n_add=1)
         self.st.x0.copy_(self.ar_tgt[:, 0])
@@ -319,9 +359,14 @@ class SelfSpecDecoder:
         with torch.cuda.graph(self.g_ar):
             self.ar_step()
 
-    def start(self, x0: torch.Tensor):
-        """Begin decoding: x0 = the token the prefill produced (committed; no K/V yet)."""
+    def start(self, x0: torch.Tensor, pos_delta: Optional[torch.Tensor] = None):
+        """Begin decoding: x0 = the token the prefill produced (committed; no K/V yet). ``pos_delta`` [bs]: the
+        position of cache index i is i + pos_delta (0 when the prompt's positions are 0..P-1)."""
         self.st.x0.copy_(x0.to(torch.int32))
+        if pos_delta is None:
+            self.pos_delta.zero_()
+        else:
+            self.pos_delta.copy_(pos_delta.to(torch.int32))
         self.st.ctr.zero_()
         self.ar_ctr.zero_()
 

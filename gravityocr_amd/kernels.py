@@ -141,6 +141,20 @@ def rope_stage(qkv, seq_lens, inv_freq, q, k_win, v_win, *, pos_offset=0, pos_de
                                _stream()), "gss_rope_stage")
 
 
+def rope_stage_mrope(qkv, positions, inv_freq, q, k_win, v_win, *, sections, rot_dim: int):
+    """One sequence's rows with explicit M-RoPE positions int32 [rows, 3]; q [rows, Hq, D]; k_win/v_win
+    [rows, Hkv, D]; ``sections`` = mrope_section (t, h, w) in rotary frequencies."""
+    rows, Hq, D = q.shape
+    Hkv = k_win.shape[1]
+    if qkv.stride(1) != 1 or qkv.shape[0] != rows or qkv.shape[1] < (Hq + 2 * Hkv) * D:
+        raise ValueError("qkv shape")
+    _need(positions, torch.int32, "positions", (rows, 3))
+    _need(inv_freq, torch.float32, "inv_freq", (rot_dim // 2,))
+    check(lib().gss_rope_stage_mrope(_ptr(qkv), qkv.stride(0), _ptr(positions), int(sections[0]), int(sections[1]),
+                                     _ptr(inv_freq), rot_dim, _ptr(q), _ptr(k_win), _ptr(v_win), rows, Hq, Hkv, D,
+                                     _stream()), "gss_rope_stage_mrope")
+
+
 def rmsnorm(x, w, out, eps):
     rows, H = x.shape
     check(lib().gss_rmsnorm(_ptr(x), _ptr(w), _ptr(out), rows, H, float(eps), _stream()), "gss_rmsnorm")

@@ -8,7 +8,7 @@ N(0, 0.02) weights with transformers' GlmOcrTextDecoderLayer attribute names, so
 from it and from a real GLM-OCR text decoder.
 """
 from dataclasses import dataclass
-from typing import Dict
+from typing import Dict, Tuple
 
 import torch
 
@@ -25,6 +25,7 @@ class GlmTextConfig:
     rms_eps: float = 1e-5
     rope_theta: float = 10000.0
     partial_rotary: float = 0.5
+    mrope_section: Tuple[int, int, int] = (8, 12, 12)   # rotary frequencies taken from the (t, h, w) positions
 
     @property
     def rot_dim(self) -> int:
@@ -70,6 +71,26 @@ def synthetic_prompt(cfg: GlmTextConfig, n_vis: int, n_text: int, seed: int):
     vis = torch.empty(n_vis, cfg.hidden).normal_(0.0, 1.0, generator=g)
     ids = torch.randint(0, cfg.vocab, (n_text,), generator=g)
     return vis, ids
+
+
+def config_from_model(model) -> GlmTextConfig:
+    """The decoder shape of a model behind the protocol: ``model.cfg`` when it is a GlmTextConfig (the synthetic
+    model), else transformers' GlmOcrTextConfig on ``model.text_model.config`` (hidden_size, num_hidden_layers,
+    num_attention_heads, num_key_value_heads, head_dim, intermediate_size, vocab_size, rms_norm_eps,
+    rope_parameters {rope_theta, partial_rotary_factor, mrope_section})."""
+    cfg = getattr(model, "cfg", None)
+    if isinstance(cfg, GlmTextConfig):
+        return cfg
+    hc = model.text_model.config
+    rp = getattr(hc, "rope_parameters", None) or {}
+    heads = hc.num_attention_heads
+    return GlmTextConfig(n_layers=hc.num_hidden_layers, hidden=hc.hidden_size, n_heads=heads,
+                         n_kv_heads=hc.num_key_value_heads,
+                         head_dim=getattr(hc, "head_dim", None) or hc.hidden_size // heads,
+                         ffn=hc.intermediate_size, vocab=hc.vocab_size, rms_eps=hc.rms_norm_eps,
+                         rope_theta=rp.get("rope_theta", 10000.0),
+                         partial_rotary=rp.get("partial_rotary_factor", 1.0),
+                         mrope_section=tuple(rp.get("mrope_section", (8, 12, 12))))
 
 
 def weights_from_model(model) -> Dict[str, torch.Tensor]:

@@ -162,6 +162,15 @@ int gss_rope_stage(const void* qkv, int64_t ld_qkv, const int32_t* seq_lens, con
                    int pos_offset, const float* inv_freq, int rot_dim, void* q, void* k_win, void* v_win, int bs,
                    int W, int Hq, int Hkv, int D, gss_stream_t stream);
 
+/* gss_rope_stage_mrope: the same split and rotation for `rows` rows of one sequence with explicit M-RoPE positions
+ * int32 [rows, 3] (t, h, w), as transformers GlmOcrTextRotaryEmbedding (modeling_glm_ocr.py:672-692): rotary
+ * frequency i uses position component 0 when i < sec_t, 1 when i < sec_t + sec_h, else 2 (mrope_section). Used by
+ * the prefill of image-token prompts, whose rows carry distinct (t, h, w) positions; the reference feeds them
+ * through _run_layers (src/fast_sampling.py:499-503). Outputs q [rows, Hq, D], window K/V [rows, Hkv, D]. */
+int gss_rope_stage_mrope(const void* qkv, int64_t ld_qkv, const int32_t* positions, int sec_t, int sec_h,
+                         const float* inv_freq, int rot_dim, void* q, void* k_win, void* v_win, int rows, int Hq,
+                         int Hkv, int D, gss_stream_t stream);
+
 /* out = rmsnorm(x) * w  (GlmOcrRMSNorm), rows x H. */
 int gss_rmsnorm(const void* x, const void* w, void* out, int rows, int H, float eps, gss_stream_t stream);
 

@@ -1,0 +1,97 @@
+"""The C-ABI library without a GPU: it loads, exports every function include/gss.h declares (and the ctypes binding
+declares exactly those), and its host-side argument checks reject bad calls before anything touches a device. The
+drop-in entry points keep the reference's signatures and reject what they do not implement, loudly."""
+import ctypes
+import inspect
+import subprocess
+
+import pytest
+import torch
+
+from gravityocr_amd import _lib
+
+OK, ARG, UNSUPPORTED, WORKSPACE = 0, 1, 2, 3
+
+
+def test_header_symbols_equal_binding():
+    syms = _lib.header_symbols()
+    assert len(syms) == len(set(syms)) >= 19
+    assert set(syms) == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in _lib.header_symbols():
+        assert hasattr(L, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(_lib.header_symbols()) <= exported
+
+
+def test_host_side_queries_and_status_strings():
+    L = _lib.lib()
+    assert L.gss_version().decode().endswith("gfx950")
+    assert L.gss_status_string(OK) == b"ok"
+    assert L.gss_status_string(WORKSPACE).startswith(b"workspace")
+    n = ctypes.c_size_t(0)
+    # argmax: counters (4 KiB) + chunk winners (value + index) of ceil(V / 4096) chunks per row
+    assert L.gss_argmax_workspace_size(2, 17, 59392, ctypes.byref(n)) == OK
+    assert n.value == 4096 + 2 * 17 * 15 * 8
+    assert L.gss_argmax_workspace_size(1, 65, 100, ctypes.byref(n)) == UNSUPPORTED
+    assert L.gss_argmax_workspace_size(0, 17, 100, ctypes.byref(n)) == ARG
+    assert L.gss_attn_workspace_size(1, 16, 2, 128, 17, 8192, ctypes.byref(n)) == OK and n.value > 0
+    assert L.gss_attn_workspace_size(1, 16, 3, 128, 17, 8192, ctypes.byref(n)) == UNSUPPORTED   # Hq % Hkv
+    assert L.gss_attn_workspace_size(1, 16, 2, 96, 17, 8192, ctypes.byref(n)) == UNSUPPORTED    # head dim
+    assert L.gss_kv_commit_workspace_size(4, ctypes.byref(n)) == OK
+
+
+def test_entry_points_reject_bad_arguments_before_launch():
+    L = _lib.lib()
+    null = None
+    # null pointers
+    assert L.gss_draft_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 17, 1, 16, 2, 128, 16, 0.1,
+                            8192, null, 0, null) == ARG
+    assert L.gss_argmax_accept(null, 0, 100, 1, 1, 100, null, null, null, null, null, null, 0, null) == ARG
+    # unsupported page size / window wider than a tile: rejected before pointers are looked at
+    assert L.gss_verify_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 17, 16, 2, 128, 32, 0.1,
+                             8192, null, 0, null) == UNSUPPORTED
+    assert L.gss_verify_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 65, 16, 2, 128, 16, 0.1,
+                             8192, null, 0, null) == UNSUPPORTED
+    assert L.gss_gemm_set_policy(0, 16) == ARG
+    assert L.gss_attn_set_split_policy(0, 2) == ARG
+
+
+REFERENCE_SIGNATURES = {
+    # src/fast_sampling.py:426-429
+    "generate_speculative_natcache": [
+        ("model", inspect.Parameter.empty), ("image", inspect.Parameter.empty), ("prompt", "Text Recognition:"),
+        ("max_new_tokens", 512), ("draft_threshold", 0.9), ("temperature", 0.0), ("top_p", 0.95),
+        ("max_long_side", 1344), ("accept_conf", 0.0), ("draft_steps", 1), ("return_stats", False),
+        ("trace", None), ("draft_bd", None), ("full_draft", True)],
+    # src/fast_sampling.py:631-632
+    "teacher_force_argmax": [("model", inspect.Parameter.empty), ("image", inspect.Parameter.empty),
+                             ("prompt", inspect.Parameter.empty), ("gen_ids", inspect.Parameter.empty),
+                             ("max_long_side", 1344)],
+    # src/fast_sampling.py:50
+    "enable_fused_flex": [("dynamic", True)],
+}
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_SIGNATURES))
+def test_dropin_signatures_match_reference(name):
+    from gravityocr_amd import fast_sampling
+    params = inspect.signature(getattr(fast_sampling, name)).parameters
+    assert [(p.name, p.default) for p in params.values()] == REFERENCE_SIGNATURES[name]
+
+
+def test_dropin_rejects_unimplemented_modes_and_cpu_models():
+    from gravityocr_amd.fast_sampling import generate_speculative_natcache
+    from gravityocr_amd.model import TINY, SyntheticGlmOcr, synthetic_prompt, synthetic_weights
+    vis, ids = synthetic_prompt(TINY, 8, 4, 0)
+    m = SyntheticGlmOcr(TINY, synthetic_weights(TINY, 0), vis, ids, mask_id=4095, bd_size=4)
+    for kw in (dict(temperature=0.7), dict(accept_conf=0.5), dict(draft_steps=2), dict(full_draft=False)):
+        with pytest.raises(NotImplementedError):
+            generate_speculative_natcache(m, None, **kw)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        generate_speculative_natcache(m, None)
