@@ -23,6 +23,8 @@ SIGNATURES = {
     "gss_argmax_accept": ([_p, _i, _i64, _i, _i, _i, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
     "gss_kv_commit_workspace_size": ([_i, _psz], _i),
     "gss_kv_commit": ([_p, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
+    "gss_ss_commit": ([_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _p], _i),
+    "gss_kv_meta": ([_p, _i64, _i64, _p, _p, _i, _p, _p, _i64, _i, _p], _i),
     "gss_gemm_set_policy": ([_i, _i], _i),
     "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p], _i),
     "gss_gemm_swiglu": ([_p, _i64, _p, _p, _i64, _p, _i, _i, _i, _p], _i),

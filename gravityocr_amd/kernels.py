@@ -128,6 +128,44 @@ def kv_commit(k_win, v_win, k_pages, v_pages, page_table, seq_lens, workspace, *
                               _stream()), "gss_kv_commit")
 
 
+def ss_commit(predict, accept_len, a0, req_pool_indices, seeds, seq_lens, loc, packed, free_slots, out, *, K: int):
+    """The serving round's commit bookkeeping (gss_ss_commit). predict int32 [>= bs*K]; accept_len int32 [bs];
+    a0 int64 [bs] (any stride); req_pool_indices int64 [bs]; seeds int64 [pool]; seq_lens int64 [bs] (in place);
+    loc int64 [bs*K]; packed int32 [bs, K+2]; free_slots int64 [bs*K]; out int64 [bs]."""
+    bs = accept_len.shape[0]
+    _need(accept_len, torch.int32, "accept_len", (bs,))
+    if predict.dtype != torch.int32 or not predict.is_contiguous() or predict.numel() < bs * K:
+        raise ValueError("predict must be contiguous int32 with at least bs*K entries")
+    if a0.dtype != torch.int64 or a0.dim() != 1 or a0.shape[0] != bs or not a0.is_cuda:
+        raise ValueError("a0 must be a GPU int64 vector of length bs")
+    _need(req_pool_indices, torch.int64, "req_pool_indices", (bs,))
+    _need(seeds, torch.int64, "seeds")
+    _need(seq_lens, torch.int64, "seq_lens", (bs,))
+    _need(loc, torch.int64, "loc", (bs * K,))
+    _need(packed, torch.int32, "packed", (bs, K + 2))
+    _need(free_slots, torch.int64, "free_slots", (bs * K,))
+    _need(out, torch.int64, "out", (bs,))
+    check(lib().gss_ss_commit(_ptr(predict), _ptr(accept_len), _ptr(a0), a0.stride(0), _ptr(req_pool_indices),
+                              _ptr(seeds), _ptr(seq_lens), _ptr(loc), _ptr(packed), _ptr(free_slots), _ptr(out),
+                              seeds.numel(), bs, K, _stream()), "gss_ss_commit")
+
+
+def kv_meta(req_to_token, req_pool_indices, seq_lens, kv_indptr, kv_indices, *, extra: int):
+    """Flattened page-size-1 KV indices of a batch (gss_kv_meta). req_to_token int32 [pool, ctx];
+    req_pool_indices / seq_lens int64 [bs]; kv_indptr int32 [bs+1]; kv_indices int32 [capacity]."""
+    bs = seq_lens.shape[0]
+    _need(req_to_token, torch.int32, "req_to_token")
+    if req_to_token.dim() != 2:
+        raise ValueError("req_to_token must be 2-D")
+    _need(req_pool_indices, torch.int64, "req_pool_indices", (bs,))
+    _need(seq_lens, torch.int64, "seq_lens", (bs,))
+    _need(kv_indptr, torch.int32, "kv_indptr", (bs + 1,))
+    _need(kv_indices, torch.int32, "kv_indices")
+    check(lib().gss_kv_meta(_ptr(req_to_token), req_to_token.shape[1], req_to_token.shape[0], _ptr(req_pool_indices),
+                            _ptr(seq_lens), int(extra), _ptr(kv_indptr), _ptr(kv_indices), kv_indices.numel(), bs,
+                            _stream()), "gss_kv_meta")
+
+
 def rope_stage(qkv, seq_lens, inv_freq, q, k_win, v_win, *, pos_offset=0, pos_delta=None, rot_dim: int):
     """qkv [bs*W, (Hq+2Hkv)*D] bf16 (row stride qkv.stride(0)); q [bs, W, Hq, D]; k_win/v_win [bs, W, Hkv, D]."""
     bs, W, Hq, D = q.shape

@@ -149,6 +149,38 @@ int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_prologue* pro
                         void* q, void* k_win, void* v_win, int bs, int W, int Hq, int Hkv, int D, int Kd,
                         gss_stream_t stream);
 
+/* ---------------------------------------------------------------- serving-boundary bookkeeping ------------------
+ * Integer steps of the SGLang round, in SGLang's buffer types, for a serving integration that keeps the pool's own
+ * request / slot layout. One wavefront per sequence; no workspace.
+ *
+ * gss_ss_commit replaces _ss_commit_kernel (patches/sglang/python/sglang/srt/speculative/selfspec_fast_commit.py:
+ * 108-147): for row i with a = accept_len[i] (clamped into [0, K-1]):
+ *   packed[i]        = (int32(a0[i * a0_stride]), a, predict[i*K .. i*K+K-1] with entries past a zeroed)
+ *   out[i]           = predict[i*K + a];  seeds[req_pool_indices[i]] = out[i]  (rows whose pool index is outside
+ *                      [0, n_seeds) leave the pool untouched)
+ *   seq_lens[i]     += a + 1
+ *   free_slots       = loc[i*K + a+1 .. i*K + K-1] of every row, compacted in row order (sum(K-1-a) entries; the
+ *                      buffer holds bs*K).
+ * K <= 64.
+ */
+int gss_ss_commit(const int32_t* predict, const int32_t* accept_len, const int64_t* a0, int64_t a0_stride,
+                  const int64_t* req_pool_indices, int64_t* seeds, int64_t* seq_lens, const int64_t* loc,
+                  int32_t* packed, int64_t* free_slots, int64_t* out, int64_t n_seeds, int bs, int K,
+                  gss_stream_t stream);
+
+/* gss_kv_meta replaces _ss_kv_meta_kernel (patches/sglang/python/sglang/srt/speculative/selfspec_fast_attn.py:
+ * 104-132): the flattened KV index list of a batch for page size 1.
+ *   n_i           = seq_lens[i] + extra, clamped into [0, r2t_stride]
+ *   kv_indptr     = [0, n_0, n_0 + n_1, ...]                                        int32 [bs + 1]
+ *   kv_indices    = req_to_token[req_pool_indices[i], 0 .. n_i-1] at kv_indptr[i]    int32
+ * req_to_token is int32 [n_req, r2t_stride]; rows whose pool index is outside [0, n_req) write no indices; entries
+ * at or past kv_indices_cap are not written (the caller sizes the buffer from its host lengths, as the reference's
+ * _meta does, selfspec_fast_attn.py:244-253).
+ */
+int gss_kv_meta(const int32_t* req_to_token, int64_t r2t_stride, int64_t n_req, const int64_t* req_pool_indices,
+                const int64_t* seq_lens, int extra, int32_t* kv_indptr, int32_t* kv_indices,
+                int64_t kv_indices_cap, int bs, gss_stream_t stream);
+
 /* ---------------------------------------------------------------- decoder-layer helpers -------------------------
  * Fused elementwise pieces of the GLM text decoder layer (transformers GlmOcrTextDecoderLayer, which the reference
  * calls through src/fast_sampling.py:89-102). bf16 in and out; fp32 inside; every step rounds to bf16 where the

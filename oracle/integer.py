@@ -135,6 +135,19 @@ def ss_commit(predict: np.ndarray, acc: np.ndarray, a0: np.ndarray, rpi: np.ndar
     return packed, seeds, seq_lens, np.asarray(free, dtype=np.int64), out
 
 
+def kv_meta(req_to_token: np.ndarray, rpi: np.ndarray, seq_lens: np.ndarray, extra: int):
+    """Restatement of ``_ss_kv_meta_kernel`` (patches/sglang/python/sglang/srt/speculative/selfspec_fast_attn.py:
+    104-132): sequence i contributes req_to_token[rpi[i], 0 : seq_lens[i] + extra] at offset
+    kv_indptr[i] = sum_{j<i} (seq_lens[j] + extra). Returns (kv_indptr int32 [bs+1], kv_indices int32)."""
+    n = [int(seq_lens[i]) + extra for i in range(len(seq_lens))]
+    indptr = np.zeros(len(n) + 1, dtype=np.int32)
+    rows = []
+    for i, ln in enumerate(n):
+        indptr[i + 1] = indptr[i] + ln
+        rows.append(np.asarray(req_to_token[int(rpi[i]), :ln], dtype=np.int32))
+    return indptr, (np.concatenate(rows) if rows else np.zeros(0, dtype=np.int32))
+
+
 def page_slot(page_table_row: np.ndarray, pos: int, page_size: int = 16) -> int:
     """Paged-KV slot of absolute position ``pos``: page_table[pos // page] * page + pos % page.
 

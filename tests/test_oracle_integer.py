@@ -6,7 +6,7 @@ import torch
 from hypothesis import given, settings
 from hypothesis import strategies as st
 
-from oracle.integer import (accept_chain, argmax_first, bf16_bits_to_f32, chain_links, committed_tokens,
+from oracle.integer import (kv_meta, accept_chain, argmax_first, bf16_bits_to_f32, chain_links, committed_tokens,
                             cut_index_loop, f32_to_bf16_bits, host_commit_loop, page_slot, ss_commit,
                             verify_tree_greedy)
 
@@ -106,6 +106,21 @@ def test_ss_commit_reference_invariants(bs, K, seed):
         assert out[i] == packed[i, 2 + a] == seeds2[rpi[i]] == predict[i * K + a]
         assert seq2[i] == seq[i] + a + 1
         assert all(packed[i, 2 + j] == 0 for j in range(a + 1, K))
+
+
+@settings(max_examples=100, deadline=None)
+@given(st.integers(1, 9), st.integers(0, 33), st.integers(0, 10**6))
+def test_kv_meta_equals_reference_host_plan_and_check(bs, extra, seed):
+    # the reference's host plan (selfspec_fast_attn.py:244-253: kv_indptr = cumsum(seq_lens_cpu + n)) and its
+    # SELFSPEC_CHECK comparison (:267-283: kv_indices == concatenated req_to_token rows), restated with numpy
+    g = np.random.default_rng(seed)
+    pool, ctx = bs + 4, 300
+    r2t = g.integers(0, 10**6, (pool, ctx)).astype(np.int32)
+    rpi = g.permutation(pool)[:bs]
+    sl = g.integers(0, ctx - extra, bs)
+    indptr, idx = kv_meta(r2t, rpi, sl, extra)
+    assert indptr.tolist() == [0] + np.cumsum(sl + extra).tolist()
+    assert idx.tolist() == np.concatenate([r2t[rpi[i], : sl[i] + extra] for i in range(bs)]).tolist()
 
 
 def test_page_slot_is_flattened_page_order():
