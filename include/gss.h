@@ -53,14 +53,17 @@ const char* gss_status_string(int status);
  *                             n_causal = 1 is the serving draft [x0 | MASK x B] and natcache rounds >= 1;
  *                             n_causal = 0 is natcache round 0 and the block-diffusion sampler's full block.
  *   verify (gss_verify_attn): row w sees window rows 0..w (causal, bottom-right aligned).
- * scale multiplies q.k (1/sqrt(D) for GLM). max_kv_len bounds L over the batch and sizes the split-KV grid;
- * the workspace must hold gss_attn_workspace_size(...) bytes and must be zeroed once after allocation (the kernels
- * leave it reusable). Supported: D in {64, 128}, page = 16, 1 <= W <= 64, Hq % Hkv == 0, Hq/Hkv * W <= 512.
+ * scale multiplies q.k (1/sqrt(D) for GLM). max_kv_len is the cache capacity: every L must be <= max_kv_len. It
+ * alone (with the split policy) fixes how the keys are partitioned, so calls with different W or L on the same
+ * cache combine every key in the same order (a verify row equals the AR step of the same token bit for bit). The
+ * workspace holds gss_attn_workspace_size(...) bytes (no zeroing needed). Supported: D in {64, 128}, page = 16,
+ * 1 <= W <= 64, Hq % Hkv == 0, max_kv_len + 64 <= 256 * 256 * 64 keys.
  */
 int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes);
 
-/* Split-KV policy of both attention kernels: about target_wgs (sequence, kv head, split) workgroups per launch, each
- * split covering at least min_tiles 64-token tiles (defaults 512 and 2). Process-wide; set before sizing workspaces. */
+/* Split-KV policy of both attention kernels: about target_wgs / (bs * Hkv) key splits per sequence and kv head, each
+ * covering at least min_tiles 64-token tiles (defaults 256 and 4; min_tiles <= 256). Process-wide; set it before
+ * sizing workspaces, and keep it fixed while a cache is decoded (it is part of the key partition). */
 int gss_attn_set_split_policy(int target_wgs, int min_tiles);
 
 int gss_draft_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int pt_stride,

@@ -15,7 +15,8 @@ from tests.helpers import ATTN_REL, PAGE, rel_err, shuffled_page_table
 pytestmark = pytest.mark.gpu
 
 
-def run_case(dev, Ls, W, n_causal, Hq=16, Hkv=2, D=128, seed=1, max_kv_len=None, prefix_extra=0, verify=False):
+def run_case(dev, Ls, W, n_causal, Hq=16, Hkv=2, D=128, seed=1, max_kv_len=None, prefix_extra=0, verify=False,
+             ws_fill=0):
     bs = len(Ls)
     g = torch.Generator().manual_seed(seed)
     sc = D ** -0.5
@@ -43,7 +44,7 @@ def run_case(dev, Ls, W, n_causal, Hq=16, Hkv=2, D=128, seed=1, max_kv_len=None,
         refs.append(masked_attention(q[b], torch.cat([k, k_win[b]]), torch.cat([v, v_win[b]]),
                                      window_mask(L, W, nc), sc))
     from gravityocr_amd.kernels import attn_workspace_bytes, window_attention
-    ws = torch.zeros(max(1, attn_workspace_bytes(bs, Hq, Hkv, D, W, cap)), dtype=torch.uint8, device=dev)
+    ws = torch.full((max(1, attn_workspace_bytes(bs, Hq, Hkv, D, W, cap)),), ws_fill, dtype=torch.uint8, device=dev)
     out = torch.empty(bs, W, Hq, D, dtype=torch.bfloat16, device=dev)
     window_attention(q.to(dev), k_pages.to(dev), v_pages.to(dev), torch.as_tensor(pt).to(dev),
                      torch.tensor(Ls, dtype=torch.int32, device=dev), k_win.to(dev), v_win.to(dev), out,
@@ -100,3 +101,23 @@ def test_deterministic(cuda):
     a, _ = run_case(cuda, [8192], 17, 1, seed=11)
     b, _ = run_case(cuda, [8192], 17, 1, seed=11)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("policy", [(1, 256), (4096, 1), (64, 9)])
+def test_split_policies(cuda, policy):
+    """One split (direct output), one tile per split (many partials), and 9-tile splits (three stages per split)."""
+    from gravityocr_amd._lib import lib
+    print(f"policy={policy}", flush=True)
+    assert lib().gss_attn_set_split_policy(*policy) == 0
+    try:
+        run_case(cuda, [5000], 17, 1, seed=21)
+        run_case(cuda, [5000, 17, 700], 17, 1, seed=22, verify=True, max_kv_len=6000)
+    finally:
+        assert lib().gss_attn_set_split_policy(256, 4) == 0
+
+
+def test_stale_workspace(cuda):
+    """The workspace is shared by calls of every window size, so split slots a call does not use hold leftovers:
+    all-ones bytes (NaN / -inf words) must not leak into the result."""
+    run_case(cuda, [1024], 17, 1, seed=31, max_kv_len=6000, ws_fill=0xFF)
+    run_case(cuda, [300, 4000], 1, 1, seed=32, max_kv_len=6000, ws_fill=0xFF, verify=True)
