@@ -25,10 +25,12 @@ SIGNATURES = {
     "gss_kv_commit": ([_p, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
     "gss_ss_commit": ([_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _p], _i),
     "gss_kv_meta": ([_p, _i64, _i64, _p, _p, _i, _p, _p, _i64, _i, _p], _i),
-    "gss_gemm_set_policy": ([_i, _i], _i),
-    "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p], _i),
-    "gss_gemm_swiglu": ([_p, _i64, _p, _p, _i64, _p, _i, _i, _i, _p], _i),
-    "gss_gemm_rope_stage": ([_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p], _i),
+    "gss_gemm_set_policy": ([_i, _i, _i], _i),
+    "gss_gemm_workspace_size": ([_i, _i, _i, _psz], _i),
+    "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p, _p, _sz, _p], _i),
+    "gss_gemm_swiglu": ([_p, _i64, _p, _p, _i64, _p, _i, _i, _i, _p, _sz, _p], _i),
+    "gss_gemm_rope_stage": ([_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz,
+                             _p], _i),
     "gss_rope_stage": ([_p, _i64, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "gss_rope_stage_mrope": ([_p, _i64, _p, _i, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _p], _i),
     "gss_rmsnorm": ([_p, _p, _p, _i, _i, _f, _p], _i),
@@ -36,6 +38,12 @@ SIGNATURES = {
     "gss_silu_mul": ([_p, _i64, _p, _i, _i, _p], _i),
 }
 
+
+
+class NormEpilogue(ctypes.Structure):
+    """gss_norm_epilogue (include/gss.h)."""
+    _fields_ = [("w_post", ctypes.c_void_p), ("h", ctypes.c_void_p), ("w_next", ctypes.c_void_p),
+                ("x", ctypes.c_void_p), ("eps", ctypes.c_float)]
 
 
 class NormPrologue(ctypes.Structure):

@@ -3,8 +3,8 @@
 // Phase 1: workgroup (chunk, row) scans 4096 logits of one row (16 per thread, 16-byte loads), keeps the best
 //   (value, index) under the greedy rule (max value, lowest index on ties, NaN as max), reduces across the
 //   wavefront with xor-shuffles and across the workgroup through LDS, and stores the chunk's winner.
-// Phase 2: the last workgroup to finish for a sequence (agent-scope release/acquire around an atomic counter in the
-//   workspace) reduces the chunk winners of each of its W rows in chunk order, then runs the linear-chain accept:
+// Phase 2: the last workgroup to finish for a sequence (chunk winners handed over through the coherence point and an
+//   atomic counter in the workspace) reduces the chunk winners of each of its W rows in chunk order, then runs the linear-chain accept:
 //   acc = leading r with target[r] == window[r+1]; next_x0 = target[acc]; packed row as the reference's readback.
 //   It then resets the counter, so the workspace needs zeroing only once and the launch is graph-replayable.
 #include "gss_common.h"
@@ -110,25 +110,25 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
     for (int w = 1; w < ARG_THREADS / 64; ++w)
       if (beats(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
     const int64_t slot = static_cast<int64_t>(row) * p.n_chunks + chunk;
-    p.part_v[slot] = bv;
-    p.part_i[slot] = bi;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const uint32_t done = __hip_atomic_fetch_add(&p.counters[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    is_last = done == static_cast<uint32_t>(p.n_chunks * p.W - 1);
+    st_agent(reinterpret_cast<uint32_t*>(p.part_v + slot), __float_as_uint(bv));
+    st_agent(reinterpret_cast<uint32_t*>(p.part_i + slot), static_cast<uint32_t>(bi));
+    wait_stores();
+    is_last = count_arrival(&p.counters[b]) == static_cast<uint32_t>(p.n_chunks * p.W - 1);
   }
   __syncthreads();
   if (!is_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 
   // ---- phase 2: this workgroup finishes sequence b ------------------------------------------------------------
   __shared__ int tgt[MAX_W];
   if (tid < p.W) {
     const int64_t base = (static_cast<int64_t>(b) * p.W + tid) * p.n_chunks;
-    float v = p.part_v[base];
-    int i = p.part_i[base];
+    const uint32_t* pv = reinterpret_cast<const uint32_t*>(p.part_v) + base;
+    const uint32_t* pi = reinterpret_cast<const uint32_t*>(p.part_i) + base;
+    float v = __uint_as_float(ld_agent(pv));
+    int i = static_cast<int>(ld_agent(pi));
     for (int c = 1; c < p.n_chunks; ++c) {
-      const float cv = p.part_v[base + c];
-      const int ci = p.part_i[base + c];
+      const float cv = __uint_as_float(ld_agent(pv + c));
+      const int ci = static_cast<int>(ld_agent(pi + c));
       if (beats(cv, ci, v, i)) { v = cv; i = ci; }
     }
     tgt[tid] = i;
@@ -153,7 +153,7 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
     if (p.packed && tid < p.W)
       p.packed[static_cast<int64_t>(b) * (p.W + 2) + 2 + tid] = tid <= acc_s ? tgt[tid] : 0;
   }
-  if (tid == 0) __hip_atomic_store(&p.counters[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) reset_counter(&p.counters[b]);
 }
 
 // Workspace layout: the per-sequence counters first (a fixed offset, whatever W and V are, so calls with different

@@ -59,16 +59,12 @@ __global__ void __launch_bounds__(COMMIT_THREADS) kv_commit_kernel(CommitParams 
     p.slots[static_cast<int64_t>(b) * p.W + tid] =
         (tid < n && pos >= 0 && pos < cap) ? pt[pos / p.page] * p.page + pos % p.page : -1;
   }
-  // the last of the n_layers workgroups of sequence b advances its length (all of them have read `base` by then)
+  // the last of the n_layers workgroups of sequence b advances its length: every workgroup has read `base` (its
+  // addresses depend on it) before it counts itself, and the new length is read only by later kernels
   __syncthreads();
-  if (tid == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const uint32_t done = __hip_atomic_fetch_add(&p.counters[b], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (done == static_cast<uint32_t>(p.n_layers - 1)) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      p.seq_lens[b] = base + n;
-      __hip_atomic_store(&p.counters[b], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  if (tid == 0 && count_arrival(&p.counters[b]) == static_cast<uint32_t>(p.n_layers - 1)) {
+    p.seq_lens[b] = base + n;
+    reset_counter(&p.counters[b]);
   }
 }
 

@@ -53,4 +53,19 @@ GSS_DEV float block_sum(float v, float* red) {
   return s;
 }
 
+// Handoffs between workgroups of one kernel (a last-arriving workgroup finishing the work of the others). The data
+// handed over is written and read with agent-scope relaxed atomics, which on gfx950 are plain vector stores / loads
+// with the sc1 bit: written through to, and read from, the coherence point shared by all XCDs. No L2 write-back or
+// invalidate is needed for it. A writer issues wait_stores() in every wave (its stores are complete), then a
+// workgroup barrier, then a relaxed counter increment; the workgroup that sees the final count reads with ld_agent.
+GSS_DEV void st_agent(uint32_t* p, uint32_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GSS_DEV void st_agent(uint64_t* p, uint64_t v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GSS_DEV uint32_t ld_agent(const uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GSS_DEV uint64_t ld_agent(const uint64_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+GSS_DEV void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+GSS_DEV uint32_t count_arrival(uint32_t* ctr) {
+  return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+GSS_DEV void reset_counter(uint32_t* ctr) { __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
 inline int gss_launch_status() { return hipGetLastError() == hipSuccess ? GSS_OK : GSS_ERR_LAUNCH; }

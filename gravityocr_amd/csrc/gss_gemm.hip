@@ -40,13 +40,25 @@ struct GemmParams {
   uint16_t* k_out;
   uint16_t* v_out;
   // prologue (PRO_ADDNORM): x = rmsnorm(h') * w_next with h' = h_in + rmsnorm(a) * w_post (a == nullptr: h' = h_in);
-  // workgroup 0 stores h' to h_out (never h_in: other workgroups still read it)
+  // workgroup (0, 0) stores h' to h_out (never h_in: other workgroups still read it)
   const uint16_t* pa;
   const uint16_t* h_in;
   uint16_t* h_out;
   const uint16_t* w_post;
   const uint16_t* w_next;
   float eps;
+  // split-K over workgroups (blockIdx.y = split): fp32 partials [ksplit][M][N] and per-column-tile counters
+  int ksplit, kps;  // splits, k-steps per split
+  float* part;
+  uint32_t* tile_ctr;
+  // post-norm epilogue (gss_norm_epilogue): the last column tile to finish runs, on every row,
+  // h = h + rmsnorm(Y) * w_post; x = rmsnorm(h) * w_next
+  uint16_t* post_h;
+  const uint16_t* post_wp;
+  const uint16_t* post_wn;
+  uint16_t* post_x;
+  float post_eps;
+  uint32_t* done_ctr;
 };
 
 constexpr int MAX_NW = 12;  // waves per workgroup (768 threads: 168 VGPRs per lane)
@@ -116,14 +128,63 @@ GSS_DEV void addnorm_row(const GemmParams& p, int row, int lane, uint16_t* xs, b
   }
 }
 
-template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8>
+// Post-norm of one row (one wavefront; H = p.N = 64 * E, E <= 32): the arithmetic, order and rounding points of
+// gss_add_rmsnorm, so the fused and separate norms agree bit for bit.
+constexpr int POST_MAX_E = 32;
+GSS_DEV void post_addnorm_row(const GemmParams& p, int row, int lane) {
+  const int E = p.N / 64;
+  const int64_t off = static_cast<int64_t>(row) * p.N + lane * E;
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.y) + off);  // E is even
+  float av[POST_MAX_E], hv[POST_MAX_E], wp[POST_MAX_E], wn[POST_MAX_E];
+#pragma unroll
+  for (int e = 0; e < POST_MAX_E; e += 2) {
+    if (e < E) {
+      const uint32_t u = ld_agent(a + e / 2);  // written by the other workgroups of this launch
+      av[e] = __uint_as_float(u << 16);
+      av[e + 1] = __uint_as_float(u & 0xffff0000u);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < POST_MAX_E; ++e) {
+    if (e < E) {
+      hv[e] = bf16_to_f32(p.post_h[off + e]);
+      wp[e] = bf16_to_f32(p.post_wp[lane * E + e]);
+      wn[e] = bf16_to_f32(p.post_wn[lane * E + e]);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < POST_MAX_E; ++e)
+    if (e < E) ss += av[e] * av[e];
+  const float ra = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(p.N) + p.post_eps);
+  float sh = 0.f;
+#pragma unroll
+  for (int e = 0; e < POST_MAX_E; ++e) {
+    if (e < E) {
+      hv[e] = round_bf16(hv[e] + round_bf16(wp[e] * round_bf16(av[e] * ra)));
+      sh += hv[e] * hv[e];
+    }
+  }
+  const float rh = 1.f / sqrtf(wave_sum(sh) / static_cast<float>(p.N) + p.post_eps);
+#pragma unroll
+  for (int e = 0; e < POST_MAX_E; ++e) {
+    if (e < E) {
+      p.post_h[off + e] = f32_to_bf16(hv[e]);
+      p.post_x[off + e] = f32_to_bf16(wn[e] * round_bf16(hv[e] * rh));
+    }
+  }
+}
+
+template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8, bool POST = false>
 __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw) {
   extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD]
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int f0 = blockIdx.x * FT * 16;
   const int ksteps = p.Kd / 32;
-  const int s_beg = wv * ksw, s_end = min(ksteps, s_beg + ksw);
+  const int ks = blockIdx.y;  // k split: k-steps [ks * kps, (ks + 1) * kps)
+  const int k_end = min(ksteps, (ks + 1) * p.kps);
+  const int s_beg = ks * p.kps + wv * ksw, s_end = min(k_end, s_beg + ksw);
 
   floatx4_t acc[FT][NT];
 #pragma unroll
@@ -162,7 +223,8 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
     }
     if constexpr (PRO == PRO_ADDNORM) {
       // the weight loads above are in flight; build the normalized rows meanwhile (single pass: ksw <= UNR)
-      for (int r = wv; r < p.M; r += NW) addnorm_row<E>(p, r, lane, xs, blockIdx.x == 0 && p.h_out != nullptr);
+      for (int r = wv; r < p.M; r += NW)
+        addnorm_row<E>(p, r, lane, xs, (blockIdx.x | blockIdx.y) == 0 && p.h_out != nullptr);
       __syncthreads();
 #pragma unroll
       for (int u = 0; u < UNR; ++u) {
@@ -203,71 +265,168 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
 #pragma unroll
     for (int n = 0; n < NT; ++n) red[((wv * FT + f) * NT + n) * 64 + lane] = acc[f][n];
   __syncthreads();
-  // wave v finishes tiles (f, n) with (f * NT + n) % NW == v
+
+  // Epilogue of tile (f, n) on its reduced sum (wave v owns the tiles with (f * NT + n) % NW == v).
+  auto epilogue = [&](int f, int n, floatx4_t s) {
+    const int row = n * 16 + l16;            // activation row
+    const int feat = f0 + f * 16 + g4 * 4;   // first of this lane's 4 consecutive output features
+    float y0 = s[0], y1 = s[1], y2 = s[2], y3 = s[3];
+    if constexpr (EPI == EPI_PLAIN) {
+      if (p.out_f32) {
+        *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) = s;
+      } else if constexpr (POST) {  // the rows are handed to the workgroup that runs the norm
+        uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy +
+                                                    feat);
+        st_agent(dst, pack_bf16x2(y0, y1));
+        st_agent(dst + 1, pack_bf16x2(y2, y3));
+      } else {
+        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) =
+            u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+      }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+      // features (gate_i, up_i, gate_i+1, up_i+1), i = feat / 2
+      const float g0 = round_bf16(y0), u0 = round_bf16(y1), g1 = round_bf16(y2), u1 = round_bf16(y3);
+      const float s0 = round_bf16(g0 / (1.f + expf(-g0))), s1 = round_bf16(g1 / (1.f + expf(-g1)));
+      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat / 2) =
+          pack_bf16x2(u0 * s0, u1 * s1);
+    } else {  // EPI_ROPE
+      const int b = row / p.W, w = row % p.W;
+      const int head = feat / p.D, d = feat % p.D;  // 4 features never straddle a head (D % 16 == 0)
+      float o[4] = {round_bf16(y0), round_bf16(y1), round_bf16(y2), round_bf16(y3)};
+      if (head < p.Hq + p.Hkv) {
+        const int pos = p.seq_lens[b] + (p.pos_delta ? p.pos_delta[b] : 0) + w;
 #pragma unroll
-  for (int f = 0; f < FT; ++f)
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      if ((f * NT + n) % NW != wv) continue;
-      floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
-      for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
-      const int row = n * 16 + l16;            // activation row
-      const int feat = f0 + f * 16 + g4 * 4;   // first of this lane's 4 consecutive output features
-      if (row >= p.M || feat >= p.N) continue;
-      float y0 = s[0], y1 = s[1], y2 = s[2], y3 = s[3];
-      if constexpr (EPI == EPI_PLAIN) {
-        if (p.out_f32) {
-          *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) = s;
-        } else {
-          *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) =
-              u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
-        }
-      } else if constexpr (EPI == EPI_SWIGLU) {
-        // features (gate_i, up_i, gate_i+1, up_i+1), i = feat / 2
-        const float g0 = round_bf16(y0), u0 = round_bf16(y1), g1 = round_bf16(y2), u1 = round_bf16(y3);
-        const float s0 = round_bf16(g0 / (1.f + expf(-g0))), s1 = round_bf16(g1 / (1.f + expf(-g1)));
-        *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat / 2) =
-            pack_bf16x2(u0 * s0, u1 * s1);
-      } else {  // EPI_ROPE
-        const int b = row / p.W, w = row % p.W;
-        const int head = feat / p.D, d = feat % p.D;  // 4 features never straddle a head (D % 16 == 0)
-        float o[4] = {round_bf16(y0), round_bf16(y1), round_bf16(y2), round_bf16(y3)};
-        if (head < p.Hq + p.Hkv) {
-          const int pos = p.seq_lens[b] + (p.pos_delta ? p.pos_delta[b] : 0) + w;
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            if (d + e < p.rot_dim) {
-              const float f = static_cast<float>(pos) * p.inv_freq[(d + e) >> 1];
-              const float c = round_bf16(cosf(f)), sn = round_bf16(sinf(f));
-              const float x0 = o[e], x1 = o[e + 1];
-              o[e] = round_bf16(round_bf16(x0 * c) - round_bf16(x1 * sn));
-              o[e + 1] = round_bf16(round_bf16(x1 * c) + round_bf16(x0 * sn));
-            }
+        for (int e = 0; e < 4; e += 2) {
+          if (d + e < p.rot_dim) {
+            const float fr = static_cast<float>(pos) * p.inv_freq[(d + e) >> 1];
+            const float c = round_bf16(cosf(fr)), sn = round_bf16(sinf(fr));
+            const float x0 = o[e], x1 = o[e + 1];
+            o[e] = round_bf16(round_bf16(x0 * c) - round_bf16(x1 * sn));
+            o[e + 1] = round_bf16(round_bf16(x1 * c) + round_bf16(x0 * sn));
           }
         }
-        uint16_t* dst;
-        if (head < p.Hq)
-          dst = p.q_out + (static_cast<int64_t>(row) * p.Hq + head) * p.D + d;
-        else if (head < p.Hq + p.Hkv)
-          dst = p.k_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq)) * p.D + d;
-        else
-          dst = p.v_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq - p.Hkv)) * p.D + d;
-        *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
       }
+      uint16_t* dst;
+      if (head < p.Hq)
+        dst = p.q_out + (static_cast<int64_t>(row) * p.Hq + head) * p.D + d;
+      else if (head < p.Hq + p.Hkv)
+        dst = p.k_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq)) * p.D + d;
+      else
+        dst = p.v_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq - p.Hkv)) * p.D + d;
+      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
     }
+  };
+  auto reduced = [&](int f, int n) {
+    floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
+    for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
+    return s;
+  };
+  auto live = [&](int f, int n) { return n * 16 + l16 < p.M && f0 + f * 16 + g4 * 4 < p.N; };
+  __shared__ int last_flag;
+
+  if (p.ksplit == 1) {
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        if ((f * NT + n) % NW == wv && live(f, n)) epilogue(f, n, reduced(f, n));
+  } else {
+    // this split's partial tile -> workspace; the last split of the column tile to arrive sums all splits in split
+    // order (agent-scope release / acquire around the counter) and runs the epilogue, then resets the counter
+    auto part_at = [&](int k, int f, int n) {
+      return reinterpret_cast<uint64_t*>(p.part + (static_cast<int64_t>(k) * p.M + n * 16 + l16) * p.N + f0 +
+                                         f * 16 + g4 * 4);
+    };
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        if ((f * NT + n) % NW == wv && live(f, n)) {
+          const floatx4_t r = reduced(f, n);
+          uint64_t* dst = part_at(ks, f, n);
+          st_agent(dst, (static_cast<uint64_t>(__float_as_uint(r[1])) << 32) | __float_as_uint(r[0]));
+          st_agent(dst + 1, (static_cast<uint64_t>(__float_as_uint(r[3])) << 32) | __float_as_uint(r[2]));
+        }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) last_flag = count_arrival(&p.tile_ctr[blockIdx.x]) == static_cast<uint32_t>(p.ksplit - 1);
+    __syncthreads();
+    if (!last_flag) return;
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        if ((f * NT + n) % NW != wv || !live(f, n)) continue;
+        floatx4_t s = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < p.ksplit; ++k) {  // split order
+          const uint64_t* src = part_at(k, f, n);
+          const uint64_t lo = ld_agent(src), hi = ld_agent(src + 1);
+          const floatx4_t v = {__uint_as_float(static_cast<uint32_t>(lo)), __uint_as_float(static_cast<uint32_t>(lo >> 32)),
+                               __uint_as_float(static_cast<uint32_t>(hi)), __uint_as_float(static_cast<uint32_t>(hi >> 32))};
+          s = k == 0 ? v : s + v;
+        }
+        epilogue(f, n, s);
+      }
+    if (tid == 0) reset_counter(&p.tile_ctr[blockIdx.x]);
+  }
+
+  if constexpr (POST) {
+    // the last column tile to finish normalizes every row (one wavefront per row), then resets the counter
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) last_flag = count_arrival(p.done_ctr) == gridDim.x - 1;
+    __syncthreads();
+    if (!last_flag) return;
+    for (int r = wv; r < p.M; r += NW) post_addnorm_row(p, r, lane);
+    if (tid == 0) reset_counter(p.done_ctr);
+  }
 }
 
-// Launch shape knobs (process-wide): the most waves per workgroup and the features per workgroup (0 = automatic).
-int g_max_nw = MAX_NW, g_ft = 0;
+// Launch shape knobs (process-wide): the most waves per workgroup, the features per workgroup (0 = automatic) and
+// the most k splits over workgroups (1 = none).
+int g_max_nw = MAX_NW, g_ft = 0, g_max_ksplit = 2;
 
-template <int FT, int NT, int EPI, int PRO>
-int launch_ft_nt(const GemmParams& p, hipStream_t st) {
-  // k-steps per wave: the fewest that cover Kd with at most g_max_nw waves (rounded to a multiple of 4)
+// Workspace: per-column-tile counters and the post-norm counter at a fixed offset (so calls of every shape share one
+// workspace), then the split-K partials.
+constexpr int CTR_TILES = 8192;
+constexpr size_t CTR_BYTES = (CTR_TILES + 64) * sizeof(uint32_t);
+
+// k splits of a (N, Kd) shape: more workgroups (up to ~384) when the column tiles alone leave CUs idle and every
+// split keeps at least 64 k-steps; below that the split's handoff (partials through the coherence point and a
+// counter) costs more than the extra streaming width buys. A function of the weight shape only, so every M runs the
+// same reduction order. For the 1536-hidden decoder: down (Kd 4608) splits in 2, the other projections do not.
+int gemm_ksplit(int n_tiles, int ksteps) {
+  int ks = max(1, min(g_max_ksplit, 384 / max(1, n_tiles)));
+  return max(1, min(ks, ksteps / 64));
+}
+
+int gemm_ft(int N) { return (g_ft == 1 || (g_ft == 0 && N / 16 <= 2048)) ? 1 : 2; }
+
+size_t gemm_ws_bytes(int M, int N, int Kd) {
+  const int ft = gemm_ft(N), n_tiles = (N + ft * 16 - 1) / (ft * 16);
+  const int ks = gemm_ksplit(n_tiles, Kd / 32);
+  return CTR_BYTES + (ks > 1 ? static_cast<size_t>(ks) * M * N * sizeof(float) : 0);
+}
+
+template <int FT, int NT, int EPI, int PRO, bool POST>
+int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
   const int ksteps = p.Kd / 32;
-  int ksw = (ksteps + g_max_nw - 1) / g_max_nw;
+  const int n_tiles = (p.N + FT * 16 - 1) / (FT * 16);
+  p.ksplit = gemm_ksplit(n_tiles, ksteps);
+  p.kps = (ksteps + p.ksplit - 1) / p.ksplit;
+  if (p.ksplit > 1 || POST) {
+    if (n_tiles > CTR_TILES) return GSS_ERR_UNSUPPORTED;
+    const size_t need = CTR_BYTES + (p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * p.M * p.N * sizeof(float) : 0);
+    if (!ws || ws_bytes < need) return GSS_ERR_WORKSPACE;
+    p.tile_ctr = static_cast<uint32_t*>(ws);
+    p.done_ctr = p.tile_ctr + CTR_TILES;
+    p.part = reinterpret_cast<float*>(static_cast<char*>(ws) + CTR_BYTES);
+  }
+  // k-steps per wave: the fewest that cover a split with at most g_max_nw waves (rounded to a multiple of 4)
+  int ksw = (p.kps + g_max_nw - 1) / g_max_nw;
   ksw = (ksw + 3) / 4 * 4;
-  const int nw = (ksteps + ksw - 1) / ksw;
-  const dim3 grid((p.N + FT * 16 - 1) / (FT * 16)), block(64 * nw);
+  const int nw = (p.kps + ksw - 1) / ksw;
+  const dim3 grid(n_tiles, p.ksplit), block(64 * nw);
   size_t lds = static_cast<size_t>(nw) * FT * NT * 64 * sizeof(floatx4_t);
   if constexpr (PRO == PRO_ADDNORM) {
     lds += static_cast<size_t>(p.M) * (p.Kd + XPAD) * sizeof(uint16_t);
@@ -284,41 +443,51 @@ int launch_ft_nt(const GemmParams& p, hipStream_t st) {
   } else {
     if constexpr (FT + NT <= 3) {
       if (ksw % 8 == 0) {
-        hipLaunchKernelGGL((gemm_kernel<FT, NT, 8, EPI>), grid, block, lds, st, p, ksw);
+        hipLaunchKernelGGL((gemm_kernel<FT, NT, 8, EPI, PRO_NONE, 8, POST>), grid, block, lds, st, p, ksw);
         return gss_launch_status();
       }
     }
-    hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI>), grid, block, lds, st, p, ksw);
+    hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO_NONE, 8, POST>), grid, block, lds, st, p, ksw);
     return gss_launch_status();
   }
 }
 
-template <int EPI, int PRO>
-int launch_epi(const GemmParams& p, hipStream_t st) {
+template <int EPI, int PRO, bool POST>
+int launch_epi(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
   const int NT = (p.M + 15) / 16;
   // 16 features per workgroup unless that makes more than ~8 workgroups per CU (the LM head)
-  if (g_ft == 1 || (g_ft == 0 && p.N / 16 <= 2048)) {
+  if (gemm_ft(p.N) == 1) {
     switch (NT) {
-      case 1: return launch_ft_nt<1, 1, EPI, PRO>(p, st);
-      case 2: return launch_ft_nt<1, 2, EPI, PRO>(p, st);
-      case 3: return launch_ft_nt<1, 3, EPI, PRO>(p, st);
-      default: return launch_ft_nt<1, 4, EPI, PRO>(p, st);
+      case 1: return launch_ft_nt<1, 1, EPI, PRO, POST>(p, ws, ws_bytes, st);
+      case 2: return launch_ft_nt<1, 2, EPI, PRO, POST>(p, ws, ws_bytes, st);
+      case 3: return launch_ft_nt<1, 3, EPI, PRO, POST>(p, ws, ws_bytes, st);
+      default: return launch_ft_nt<1, 4, EPI, PRO, POST>(p, ws, ws_bytes, st);
     }
   }
-  switch (NT) {
-    case 1: return launch_ft_nt<2, 1, EPI, PRO>(p, st);
-    case 2: return launch_ft_nt<2, 2, EPI, PRO>(p, st);
-    case 3: return launch_ft_nt<2, 3, EPI, PRO>(p, st);
-    default: return launch_ft_nt<2, 4, EPI, PRO>(p, st);
+  if constexpr (POST) {
+    return GSS_ERR_UNSUPPORTED;  // the post-norm runs on hidden-size outputs only
+  } else {
+    switch (NT) {
+      case 1: return launch_ft_nt<2, 1, EPI, PRO, false>(p, ws, ws_bytes, st);
+      case 2: return launch_ft_nt<2, 2, EPI, PRO, false>(p, ws, ws_bytes, st);
+      case 3: return launch_ft_nt<2, 3, EPI, PRO, false>(p, ws, ws_bytes, st);
+      default: return launch_ft_nt<2, 4, EPI, PRO, false>(p, ws, ws_bytes, st);
+    }
   }
 }
 
-int gemm_entry(GemmParams& p, int epi, hipStream_t st) {
-  const bool pro = p.h_in != nullptr;
+int gemm_entry(GemmParams& p, int epi, void* ws, size_t ws_bytes, hipStream_t st) {
+  const bool pro = p.h_in != nullptr, post = p.post_h != nullptr;
   if ((!pro && !p.x) || !p.w || p.M <= 0 || p.N <= 0 || p.Kd <= 0) return GSS_ERR_ARG;
   if (p.M > 64 || p.Kd % 32 != 0 || p.N % 16 != 0) return GSS_ERR_UNSUPPORTED;
   if (p.ldw < p.Kd || (p.ldw % 8) || (!pro && (p.ldx < p.Kd || (p.ldx % 8)))) return GSS_ERR_ARG;
   if ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.w)) & 15u) return GSS_ERR_ARG;
+  if (post) {
+    if (pro || epi != EPI_PLAIN || p.out_f32 || p.ldy != p.N) return GSS_ERR_ARG;
+    if (!p.post_wp || !p.post_wn || !p.post_x || p.post_x == p.post_h) return GSS_ERR_ARG;
+    if (p.N % 128 != 0 || p.N / 64 > POST_MAX_E) return GSS_ERR_UNSUPPORTED;  // an even count per lane
+    return launch_epi<EPI_PLAIN, PRO_NONE, true>(p, ws, ws_bytes, st);
+  }
   if (pro) {
     if (!p.w_next || (p.pa && !p.w_post) || p.h_out == p.h_in) return GSS_ERR_ARG;
     if (p.Kd % 512 != 0) return GSS_ERR_UNSUPPORTED;  // 8-element chunks per lane
@@ -327,15 +496,15 @@ int gemm_entry(GemmParams& p, int epi, hipStream_t st) {
          reinterpret_cast<uintptr_t>(p.w_post)) & 15u)
       return GSS_ERR_ARG;
     switch (epi) {
-      case EPI_PLAIN: return launch_epi<EPI_PLAIN, PRO_ADDNORM>(p, st);
-      case EPI_SWIGLU: return launch_epi<EPI_SWIGLU, PRO_ADDNORM>(p, st);
-      default: return launch_epi<EPI_ROPE, PRO_ADDNORM>(p, st);
+      case EPI_PLAIN: return launch_epi<EPI_PLAIN, PRO_ADDNORM, false>(p, ws, ws_bytes, st);
+      case EPI_SWIGLU: return launch_epi<EPI_SWIGLU, PRO_ADDNORM, false>(p, ws, ws_bytes, st);
+      default: return launch_epi<EPI_ROPE, PRO_ADDNORM, false>(p, ws, ws_bytes, st);
     }
   }
   switch (epi) {
-    case EPI_PLAIN: return launch_epi<EPI_PLAIN, PRO_NONE>(p, st);
-    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU, PRO_NONE>(p, st);
-    default: return launch_epi<EPI_ROPE, PRO_NONE>(p, st);
+    case EPI_PLAIN: return launch_epi<EPI_PLAIN, PRO_NONE, false>(p, ws, ws_bytes, st);
+    case EPI_SWIGLU: return launch_epi<EPI_SWIGLU, PRO_NONE, false>(p, ws, ws_bytes, st);
+    default: return launch_epi<EPI_ROPE, PRO_NONE, false>(p, ws, ws_bytes, st);
   }
 }
 
@@ -352,8 +521,15 @@ void set_prologue(GemmParams& p, const gss_norm_prologue* pro) {
 
 }  // namespace
 
+extern "C" int gss_gemm_workspace_size(int M, int N, int Kd, size_t* bytes) {
+  if (!bytes || M <= 0 || N <= 0 || Kd <= 0) return GSS_ERR_ARG;
+  *bytes = gemm_ws_bytes(M, N, Kd);
+  return GSS_OK;
+}
+
 extern "C" int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w, int64_t ldw, void* y,
-                        int64_t ldy, int M, int N, int Kd, int out_dtype, gss_stream_t stream) {
+                        int64_t ldy, int M, int N, int Kd, int out_dtype, const gss_norm_epilogue* post,
+                        void* workspace, size_t workspace_bytes, gss_stream_t stream) {
   if (!y || ldy < N || (out_dtype != GSS_BF16 && out_dtype != GSS_F32)) return GSS_ERR_ARG;
   if ((ldy % 4) || (reinterpret_cast<uintptr_t>(y) & 15u)) return GSS_ERR_ARG;
   GemmParams p = {};
@@ -368,11 +544,20 @@ extern "C" int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro
   p.Kd = Kd;
   p.out_f32 = out_dtype == GSS_F32;
   set_prologue(p, pro);
-  return gemm_entry(p, EPI_PLAIN, static_cast<hipStream_t>(stream));
+  if (post != nullptr) {
+    if (!post->h) return GSS_ERR_ARG;
+    p.post_h = static_cast<uint16_t*>(post->h);
+    p.post_wp = static_cast<const uint16_t*>(post->w_post);
+    p.post_wn = static_cast<const uint16_t*>(post->w_next);
+    p.post_x = static_cast<uint16_t*>(post->x);
+    p.post_eps = post->eps;
+  }
+  return gemm_entry(p, EPI_PLAIN, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int gss_gemm_swiglu(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_gu_interleaved,
-                               int64_t ldw, void* act, int M, int F, int Kd, gss_stream_t stream) {
+                               int64_t ldw, void* act, int M, int F, int Kd, void* workspace, size_t workspace_bytes,
+                               gss_stream_t stream) {
   if (!act || (reinterpret_cast<uintptr_t>(act) & 3u)) return GSS_ERR_ARG;
   GemmParams p = {};
   p.x = static_cast<const uint16_t*>(x);
@@ -385,13 +570,14 @@ extern "C" int gss_gemm_swiglu(const void* x, int64_t ldx, const gss_norm_prolog
   p.N = 2 * F;
   p.Kd = Kd;
   set_prologue(p, pro);
-  return gemm_entry(p, EPI_SWIGLU, static_cast<hipStream_t>(stream));
+  return gemm_entry(p, EPI_SWIGLU, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_qkv,
                                    int64_t ldw, const int32_t* seq_lens, const int32_t* pos_delta,
                                    const float* inv_freq, int rot_dim, void* q, void* k_win, void* v_win, int bs,
-                                   int W, int Hq, int Hkv, int D, int Kd, gss_stream_t stream) {
+                                   int W, int Hq, int Hkv, int D, int Kd, void* workspace, size_t workspace_bytes,
+                                   gss_stream_t stream) {
   if (!seq_lens || !inv_freq || !q || !k_win || !v_win || bs <= 0 || W <= 0) return GSS_ERR_ARG;
   if (D % 16 != 0 || rot_dim < 0 || rot_dim > D || rot_dim % 2) return GSS_ERR_ARG;
   GemmParams p = {};
@@ -415,13 +601,15 @@ extern "C" int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_pr
   p.k_out = static_cast<uint16_t*>(k_win);
   p.v_out = static_cast<uint16_t*>(v_win);
   set_prologue(p, pro);
-  return gemm_entry(p, EPI_ROPE, static_cast<hipStream_t>(stream));
+  return gemm_entry(p, EPI_ROPE, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int gss_gemm_set_policy(int max_waves, int features_per_wg) {
+extern "C" int gss_gemm_set_policy(int max_waves, int features_per_wg, int max_ksplit) {
   if (max_waves < 1 || max_waves > MAX_NW || (features_per_wg != 0 && features_per_wg != 16 && features_per_wg != 32))
     return GSS_ERR_ARG;
+  if (max_ksplit < 1 || max_ksplit > 8) return GSS_ERR_ARG;
   g_max_nw = max_waves;
   g_ft = features_per_wg / 16;
+  g_max_ksplit = max_ksplit;
   return GSS_OK;
 }

@@ -55,7 +55,11 @@ class GssEngine:
         self.cfg = cfg
         # "gss": the batch-invariant skinny GEMMs (rows <= 64); "torch": hipBLASLt through torch.mm everywhere
         self.gemm_impl = gemm
-        self.fuse_norm_rows = 4
+        # the GEMM prologue norm is bit-identical only to an unsplit GEMM; the decode path normalizes in the GEMM
+        # epilogues instead, for every row count (0 = the prologue path is off)
+        self.fuse_norm_rows = 0
+        # sandwich norms in the o_proj / down GEMM epilogues (one launch less each) instead of gss_add_rmsnorm
+        self.post_norm = False
         self.device = torch.device(device)
         self.max_bs, self.max_len, self.max_win = max_bs, max_len, max_win
         dev, bf = self.device, torch.bfloat16
@@ -95,6 +99,11 @@ class GssEngine:
                                                                  max_win, max_len)), dtype=torch.uint8, device=dev)
         self.ws_arg = torch.zeros(K.argmax_workspace_bytes(max_bs, max_win, cfg.vocab), dtype=torch.uint8, device=dev)
         self.ws_commit = torch.zeros(K.commit_workspace_bytes(max_bs), dtype=torch.uint8, device=dev)
+        rows = min(64, max_bs * max_win)
+        shapes = [(cfg.qkv_dim, cfg.hidden), (cfg.hidden, cfg.n_heads * cfg.head_dim), (2 * cfg.ffn, cfg.hidden),
+                  (cfg.hidden, cfg.ffn), (cfg.vocab, cfg.hidden)]
+        self.ws_gemm = torch.zeros(max(K.gemm_workspace_bytes(rows, n, kd) for n, kd in shapes), dtype=torch.uint8,
+                                   device=dev)
         self._bufs: Dict[Tuple[int, int], _Bufs] = {}
 
     # ------------------------------------------------------------------------------------------ primitives ------
@@ -122,37 +131,54 @@ class GssEngine:
         else:
             torch.index_select(self.embed, 0, ids.reshape(-1), out=b.h)
         own = self.gemm_impl == "gss" and bs * W <= 64
-        # norms folded into the GEMM prologues pay off only for a few rows (each workgroup re-normalizes every row)
+        # the GEMM-prologue norm path (off by default: it would not match the split-K epilogue path bit for bit)
         if own and bs * W <= self.fuse_norm_rows and c.hidden % 512 == 0 and c.hidden <= 1536:
             return self._forward_fused(b, n_causal, sl, pt, pos_delta, mkl)
         K.rmsnorm(b.h, self.n_in[0], b.x, c.rms_eps)
+        if own:
+            return self._forward_own(b, n_causal, sl, pt, pos_delta, mkl)
+        # more than 64 rows (or gemm="torch"): hipBLASLt GEMMs and the separate norm kernels
         for l in range(c.n_layers):
-            if own:
-                K.gemm_rope_stage(b.x, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l],
-                                  rot_dim=c.rot_dim, pos_delta=pos_delta)
-            else:
-                torch.mm(b.x, self.wqkv[l].t(), out=b.qkv)
-                K.rope_stage(b.qkv, sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], pos_delta=pos_delta,
-                             rot_dim=c.rot_dim)
+            torch.mm(b.x, self.wqkv[l].t(), out=b.qkv)
+            K.rope_stage(b.qkv, sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], pos_delta=pos_delta,
+                         rot_dim=c.rot_dim)
             K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
                                n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
-            if own:
-                K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a)
-            else:
-                torch.mm(b.o.view(bs * W, -1), self.wo[l].t(), out=b.a)
+            torch.mm(b.o.view(bs * W, -1), self.wo[l].t(), out=b.a)
             K.add_rmsnorm(b.a, self.n_psa[l], b.h, self.n_pa[l], b.x, c.rms_eps)
-            if own:
-                K.gemm_swiglu(b.x, self.wgu[l], b.act)
-                K.gemm(b.act, self.wdown[l], b.a)
-            else:
-                self._swiglu_torch(b.x, self.wgu[l], b.gu, b.act)
-                torch.mm(b.act, self.wdown[l].t(), out=b.a)
+            self._swiglu_torch(b.x, self.wgu[l], b.gu, b.act)
+            torch.mm(b.act, self.wdown[l].t(), out=b.a)
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
             K.add_rmsnorm(b.a, self.n_pm[l], b.h, nxt, b.x, c.rms_eps)
-        if own:
-            K.gemm(b.x, self.lm_head, b.logits)
-        else:
-            torch.mm(b.x, self.lm_head.t(), out=b.logits)
+        torch.mm(b.x, self.lm_head.t(), out=b.logits)
+        return b.logits.view(bs, W, c.vocab)
+
+    def _forward_own(self, b: _Bufs, n_causal, sl, pt, pos_delta, mkl) -> torch.Tensor:
+        """Decode forward on the batch-invariant GEMMs (b.x already holds the first input norm). Per layer:
+        [qkv + RoPE + staging], attention (+ split merge), o_proj, residual norm, [gate_up + SwiGLU], down,
+        residual norm (the norms inside the o_proj / down GEMM epilogues when post_norm is set)."""
+        c = self.cfg
+        bs, W = b.bs, b.W
+        ws = self.ws_gemm
+        for l in range(c.n_layers):
+            K.gemm_rope_stage(b.x, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], rot_dim=c.rot_dim,
+                              pos_delta=pos_delta, workspace=ws)
+            K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
+                               n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
+            nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
+            if self.post_norm:
+                K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a, workspace=ws,
+                       post=dict(h=b.h, w_post=self.n_psa[l], w_next=self.n_pa[l], x=b.x, eps=c.rms_eps))
+                K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
+                K.gemm(b.act, self.wdown[l], b.a, workspace=ws,
+                       post=dict(h=b.h, w_post=self.n_pm[l], w_next=nxt, x=b.x, eps=c.rms_eps))
+            else:
+                K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a, workspace=ws)
+                K.add_rmsnorm(b.a, self.n_psa[l], b.h, self.n_pa[l], b.x, c.rms_eps)
+                K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
+                K.gemm(b.act, self.wdown[l], b.a, workspace=ws)
+                K.add_rmsnorm(b.a, self.n_pm[l], b.h, nxt, b.x, c.rms_eps)
+        K.gemm(b.x, self.lm_head, b.logits, workspace=ws)
         return b.logits.view(bs, W, c.vocab)
 
     def _forward_fused(self, b: _Bufs, n_causal, sl, pt, pos_delta, mkl) -> torch.Tensor:

@@ -5,7 +5,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import NormPrologue, check, lib
+from ._lib import NormEpilogue, NormPrologue, check, lib
 
 PAGE = 16
 
@@ -239,9 +239,44 @@ def _rows(x, pro):
     return (x.shape[0], x.stride(0)) if x is not None else (pro["h_in"].shape[0], 0)
 
 
-def gemm(x, w, y, pro=None):
+def gemm_workspace_bytes(M, N, Kd) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().gss_gemm_workspace_size(M, N, Kd, ctypes.byref(n)), "gss_gemm_workspace_size")
+    return n.value
+
+
+_DEFAULT_WS = {}
+
+
+def _gemm_ws(workspace, dev, M, N, Kd):
+    """The caller's GEMM workspace, or (callers that do not keep one, e.g. tests) a zeroed per-device default that
+    grows to the largest shape seen."""
+    if workspace is not None:
+        return workspace
+    need = gemm_workspace_bytes(M, N, Kd)
+    ws = _DEFAULT_WS.get(dev)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+        _DEFAULT_WS[dev] = ws
+    return ws
+
+
+def _epilogue(post, M, N):
+    """post = dict(h=..., w_post=..., w_next=..., x=..., eps=...) -> NormEpilogue or None."""
+    if post is None:
+        return None
+    for k in ("h", "x"):
+        _need(post[k], torch.bfloat16, f"epilogue {k}", (M, N))
+    for k in ("w_post", "w_next"):
+        _need(post[k], torch.bfloat16, f"epilogue {k}", (N,))
+    return NormEpilogue(_ptr(post["w_post"]).value, _ptr(post["h"]).value, _ptr(post["w_next"]).value,
+                        _ptr(post["x"]).value, float(post["eps"]))
+
+
+def gemm(x, w, y, pro=None, post=None, workspace=None):
     """y[M, N] = x[M, Kd] @ w[N, Kd]^T (bf16 or fp32 y), M <= 64, batch invariant. With ``pro`` (a dict of the
-    gss_norm_prologue fields) x is rmsnorm(h_in + rmsnorm(a) * w_post) * w_next, built inside the kernel."""
+    gss_norm_prologue fields) x is rmsnorm(h_in + rmsnorm(a) * w_post) * w_next, built inside the kernel; with
+    ``post`` (gss_norm_epilogue fields) the kernel finishes with h += rmsnorm(y) * w_post, x = rmsnorm(h) * w_next."""
     _gemm_args(x, w)
     Kd, N = w.shape[1], w.shape[0]
     M, ldx = _rows(x, pro)
@@ -249,22 +284,28 @@ def gemm(x, w, y, pro=None):
         raise ValueError("gemm output shape")
     dt = {torch.bfloat16: 0, torch.float32: 1}[y.dtype]
     pr = _prologue(pro, M, Kd)
+    po = _epilogue(post, M, N)
+    ws = _gemm_ws(workspace, w.device, M, N, Kd)
     check(lib().gss_gemm(_ptr(x), ldx, None if pr is None else ctypes.byref(pr), _ptr(w), w.stride(0), _ptr(y),
-                         y.stride(0), M, N, Kd, dt, _stream()), "gss_gemm")
+                         y.stride(0), M, N, Kd, dt, None if po is None else ctypes.byref(po), _ptr(ws),
+                         ws.numel(), _stream()), "gss_gemm")
 
 
-def gemm_swiglu(x, w_gu_il, act, pro=None):
+def gemm_swiglu(x, w_gu_il, act, pro=None, workspace=None):
     """act[M, F] = up * silu(gate) of x @ w_gu_il^T, w_gu_il [2F, Kd] with gate/up rows interleaved."""
     _gemm_args(x, w_gu_il)
     Kd, F = w_gu_il.shape[1], w_gu_il.shape[0] // 2
     M, ldx = _rows(x, pro)
     _need(act, torch.bfloat16, "act", (M, F))
     pr = _prologue(pro, M, Kd)
+    ws = _gemm_ws(workspace, w_gu_il.device, M, 2 * F, Kd)
     check(lib().gss_gemm_swiglu(_ptr(x), ldx, None if pr is None else ctypes.byref(pr), _ptr(w_gu_il),
-                                w_gu_il.stride(0), _ptr(act), M, F, Kd, _stream()), "gss_gemm_swiglu")
+                                w_gu_il.stride(0), _ptr(act), M, F, Kd, _ptr(ws), ws.numel(), _stream()),
+          "gss_gemm_swiglu")
 
 
-def gemm_rope_stage(x, w_qkv, seq_lens, inv_freq, q, k_win, v_win, *, rot_dim, pos_delta=None, pro=None):
+def gemm_rope_stage(x, w_qkv, seq_lens, inv_freq, q, k_win, v_win, *, rot_dim, pos_delta=None, pro=None,
+                    workspace=None):
     """q|k|v projection with RoPE and window staging fused: q [bs, W, Hq, D], k_win/v_win [bs, W, Hkv, D]."""
     _gemm_args(x, w_qkv)
     bs, W, Hq, D = q.shape
@@ -278,7 +319,9 @@ def gemm_rope_stage(x, w_qkv, seq_lens, inv_freq, q, k_win, v_win, *, rot_dim, p
     _need(k_win, torch.bfloat16, "k_win", (bs, W, Hkv, D))
     _need(v_win, torch.bfloat16, "v_win", (bs, W, Hkv, D))
     pr = _prologue(pro, M, Kd)
+    ws = _gemm_ws(workspace, w_qkv.device, M, w_qkv.shape[0], Kd)
     check(lib().gss_gemm_rope_stage(_ptr(x), ldx, None if pr is None else ctypes.byref(pr), _ptr(w_qkv),
                                     w_qkv.stride(0), _ptr(seq_lens), _ptr(pos_delta), _ptr(inv_freq), rot_dim,
-                                    _ptr(q), _ptr(k_win), _ptr(v_win), bs, W, Hq, Hkv, D, Kd, _stream()),
+                                    _ptr(q), _ptr(k_win), _ptr(v_win), bs, W, Hq, Hkv, D, Kd, _ptr(ws), ws.numel(),
+                                    _stream()),
           "gss_gemm_rope_stage")

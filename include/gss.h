@@ -138,19 +138,41 @@ typedef struct gss_norm_prologue {
 } gss_norm_prologue;
 
 /* Launch-shape policy of the three GEMMs (process-wide): at most max_waves (1..12) waves per workgroup splitting
- * Kd, and features_per_wg output features per workgroup (16 or 32; 0 = 16 unless N > 32768). */
-int gss_gemm_set_policy(int max_waves, int features_per_wg);
+ * Kd, features_per_wg output features per workgroup (16 or 32; 0 = 16 unless N > 32768), and at most max_ksplit
+ * (1..8) k splits over workgroups for shapes with few column tiles and at least 64 k-steps per split (default 2).
+ * The split count is part of the reduction order: keep the policy fixed while a cache is decoded. */
+int gss_gemm_set_policy(int max_waves, int features_per_wg, int max_ksplit);
+
+/* Norm epilogue of gss_gemm (the sandwich norm after o_proj and after the MLP down projection,
+ * modeling_glm_ocr.py:263-310): once Y = X W^T is written (bf16, ldy == N, N = hidden size), every row gets
+ *   h = h + rmsnorm(Y) * w_post;   x = rmsnorm(h) * w_next
+ * with the arithmetic of gss_add_rmsnorm (bit-identical results). h is updated in place. */
+typedef struct gss_norm_epilogue {
+  const void* w_post;
+  void* h;
+  const void* w_next;
+  void* x;
+  float eps;
+} gss_norm_epilogue;
+
+/* Workspace of the three GEMMs: per-column-tile counters at a fixed offset (zero them once after allocation; the
+ * kernels leave them at zero) and the split-K partials of shapes whose column tiles alone would leave most CUs idle
+ * (the k split depends on N and Kd only, never on M, so results stay batch invariant). One workspace sized for the
+ * largest (M, N, Kd) serves every call on a stream. */
+int gss_gemm_workspace_size(int M, int N, int Kd, size_t* bytes);
 
 int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w, int64_t ldw, void* y,
-             int64_t ldy, int M, int N, int Kd, int out_dtype, gss_stream_t stream);
+             int64_t ldy, int M, int N, int Kd, int out_dtype, const gss_norm_epilogue* post, void* workspace,
+             size_t workspace_bytes, gss_stream_t stream);
 
 int gss_gemm_swiglu(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_gu_interleaved,
-                    int64_t ldw, void* act, int M, int F, int Kd, gss_stream_t stream);
+                    int64_t ldw, void* act, int M, int F, int Kd, void* workspace, size_t workspace_bytes,
+                    gss_stream_t stream);
 
 int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_qkv, int64_t ldw,
                         const int32_t* seq_lens, const int32_t* pos_delta, const float* inv_freq, int rot_dim,
                         void* q, void* k_win, void* v_win, int bs, int W, int Hq, int Hkv, int D, int Kd,
-                        gss_stream_t stream);
+                        void* workspace, size_t workspace_bytes, gss_stream_t stream);
 
 /* ---------------------------------------------------------------- serving-boundary bookkeeping ------------------
  * Integer steps of the SGLang round, in SGLang's buffer types, for a serving integration that keeps the pool's own

@@ -58,7 +58,8 @@ def test_entry_points_reject_bad_arguments_before_launch():
                              8192, null, 0, null) == UNSUPPORTED
     assert L.gss_verify_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 65, 16, 2, 128, 16, 0.1,
                              8192, null, 0, null) == UNSUPPORTED
-    assert L.gss_gemm_set_policy(0, 16) == ARG
+    assert L.gss_gemm_set_policy(0, 16, 1) == ARG
+    assert L.gss_gemm_set_policy(12, 16, 9) == ARG
     assert L.gss_attn_set_split_policy(0, 2) == ARG
 
 
@@ -95,3 +96,27 @@ def test_dropin_rejects_unimplemented_modes_and_cpu_models():
             generate_speculative_natcache(m, None, **kw)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         generate_speculative_natcache(m, None)
+
+
+def test_gemm_workspace_sizes_follow_the_k_split():
+    """With k splits allowed, split-K partials only for shapes whose column tiles leave CUs idle and whose splits keep
+    at least 64 k-steps (the down projection of the 1536-hidden decoder); the counters' block is always there."""
+    L = _lib.lib()
+    n = ctypes.c_size_t(0)
+    sizes = {}
+    assert L.gss_gemm_set_policy(12, 0, 1) == OK
+    assert L.gss_gemm_workspace_size(17, 1536, 4608, ctypes.byref(n)) == OK
+    unsplit = n.value                                        # no k split allowed
+    assert L.gss_gemm_set_policy(12, 0, 8) == OK
+    try:
+        for N, Kd in [(2560, 1536), (1536, 2048), (9216, 1536), (1536, 4608), (59392, 1536)]:
+            assert L.gss_gemm_workspace_size(17, N, Kd, ctypes.byref(n)) == OK
+            sizes[(N, Kd)] = n.value
+    finally:
+        assert L.gss_gemm_set_policy(12, 0, 2) == OK
+    assert unsplit == sizes[(9216, 1536)]
+    ctr = sizes[(9216, 1536)]
+    assert sizes[(59392, 1536)] == ctr                          # many column tiles: unsplit
+    assert sizes[(2560, 1536)] == ctr                          # 48 k-steps: too short to split
+    assert sizes[(1536, 2048)] == ctr                          # 64 k-steps: one split of 64
+    assert sizes[(1536, 4608)] == ctr + 2 * 17 * 1536 * 4      # 144 k-steps, 96 column tiles -> 2 splits

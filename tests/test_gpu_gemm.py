@@ -132,3 +132,74 @@ def test_norm_prologue_equals_unfused(cuda, M):
     gemm_swiglu(None, wgu, act, pro=dict(h_in=h, w_next=wn, eps=eps))
     torch.cuda.synchronize()
     assert torch.equal(act, act_ref)
+
+
+@pytest.fixture(params=[1, 8], ids=["unsplit", "ksplit"])
+def ksplit_policy(request):
+    """The GEMM policy with k splits off and allowed up to 8 (the default, 2, is restored afterwards)."""
+    from gravityocr_amd._lib import lib
+    assert lib().gss_gemm_set_policy(12, 0, request.param) == 0
+    yield request.param
+    assert lib().gss_gemm_set_policy(12, 0, 2) == 0
+
+
+@pytest.mark.parametrize("M,N,Kd", [(17, 2560, 1536), (1, 1536, 2048), (17, 1536, 4608), (64, 1536, 4608)])
+def test_gemm_split_k_parity_and_invariance(cuda, ksplit_policy, M, N, Kd):
+    """Split-K keeps fp32-reference parity and batch invariance (a row alone == the same row in a batch)."""
+    from gravityocr_amd.kernels import gemm
+    g = torch.Generator().manual_seed(M + N + Kd)
+    x = torch.randn(M, Kd, generator=g).bfloat16().to(cuda)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).bfloat16().to(cuda)
+    y = torch.empty(M, N, dtype=torch.float32, device=cuda)
+    gemm(x, w, y)
+    y1 = torch.empty(1, N, dtype=torch.float32, device=cuda)
+    gemm(x[M - 1:].contiguous(), w, y1)
+    torch.cuda.synchronize()
+    r = ref(x, w)
+    assert float((y - r).abs().max()) <= 1e-4 * float(r.abs().max()) + 1e-5
+    assert torch.equal(y1[0], y[M - 1])
+
+
+@pytest.mark.parametrize("M", [1, 17, 64])
+@pytest.mark.parametrize("N,Kd", [(1536, 2048), (1536, 4608), (256, 704)])
+def test_post_norm_epilogue_equals_separate_norm(cuda, ksplit_policy, M, N, Kd):
+    """gss_norm_epilogue (h += rmsnorm(Y) * w_post; x = rmsnorm(h) * w_next inside the GEMM) == the plain GEMM followed
+    by gss_add_rmsnorm, bit for bit, for split-K (N = 1536) and unsplit shapes."""
+    from gravityocr_amd.kernels import add_rmsnorm, gemm
+    g = torch.Generator().manual_seed(M * 3 + N + Kd)
+    x = torch.randn(M, Kd, generator=g).bfloat16().to(cuda)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).bfloat16().to(cuda)
+    h = torch.randn(M, N, generator=g).bfloat16().to(cuda)
+    wp = (1 + 0.1 * torch.randn(N, generator=g)).bfloat16().to(cuda)
+    wn = (1 + 0.1 * torch.randn(N, generator=g)).bfloat16().to(cuda)
+    a_ref = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+    gemm(x, w, a_ref)
+    h_ref, x_ref = h.clone(), torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+    add_rmsnorm(a_ref, wp, h_ref, wn, x_ref, 1e-5)
+    ws = torch.zeros(1 << 22, dtype=torch.uint8, device=cuda)
+    for rep in range(3):  # the counters reset themselves: repeated calls on one workspace agree
+        a, h2, x2 = torch.empty_like(a_ref), h.clone(), torch.empty_like(x_ref)
+        gemm(x, w, a, workspace=ws, post=dict(h=h2, w_post=wp, w_next=wn, x=x2, eps=1e-5))
+        torch.cuda.synchronize()
+        assert torch.equal(a, a_ref) and torch.equal(h2, h_ref) and torch.equal(x2, x_ref), rep
+
+
+def test_split_k_shapes_share_one_workspace(cuda, ksplit_policy):
+    """The decoder's GEMM shapes one after another on one workspace (split and unsplit, different tile counts) give
+    the results of the same calls on fresh workspaces."""
+    from gravityocr_amd.kernels import gemm, gemm_workspace_bytes
+    g = torch.Generator().manual_seed(77)
+    shapes = [(2560, 1536), (1536, 2048), (9216, 1536), (1536, 4608), (59392, 1536)]
+    M = 17
+    xs = {kd: torch.randn(M, kd, generator=g).bfloat16().to(cuda) for kd in {kd for _, kd in shapes}}
+    ws_all = [(torch.randn(n, kd, generator=g) * 0.02).bfloat16().to(cuda) for n, kd in shapes]
+    shared = torch.zeros(max(gemm_workspace_bytes(M, n, kd) for n, kd in shapes), dtype=torch.uint8, device=cuda)
+    for rep in range(2):
+        for (n, kd), w in zip(shapes, ws_all):
+            y1 = torch.empty(M, n, dtype=torch.bfloat16, device=cuda)
+            gemm(xs[kd], w, y1, workspace=shared)
+            y2 = torch.empty_like(y1)
+            gemm(xs[kd], w, y2, workspace=torch.zeros(gemm_workspace_bytes(M, n, kd), dtype=torch.uint8,
+                                                       device=cuda))
+            torch.cuda.synchronize()
+            assert torch.equal(y1, y2), (rep, n, kd)
