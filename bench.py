@@ -10,7 +10,8 @@ Reported next to it, in the same JSON line:
   * AR decode of the same model on the same GPU (one 1-row forward per token, also graph-replayed);
   * planted-acceptance rounds: the draft is overwritten with the AR tokens up to a mismatch ~ geometric(0.1)
     (capped at B), so the verify accepts what a trained draft would (kernel cost per round does not depend on it);
-  * roofline of the block-diffusion draft attention kernel at the round's shape (HIP events on its stream);
+  * roofline of the block-diffusion draft attention at the round's shape (HIP events on its stream), timed over 48
+    distinct caches so its K/V comes from HBM (`--attn-only` runs just this measurement, for rocprof);
   * the CPU baseline: the oracle's full-draft round (fp32 torch) on the host cores, from the same 8K state.
 
     python bench.py [--steps K] [--warmup W] [--no-cpu] [--prefix 8192] [--tokens 512] [--bd 16]
@@ -41,15 +42,68 @@ def attn_flops(L, W, Hq=16, D=128):
     return 4 * W * Hq * D * (L + W)
 
 
+ATTN_COPIES = 48  # distinct KV caches the attention timing cycles through (48 x 8.7 MB > the 256 MB Infinity Cache)
+COPY_BYTES = 64 << 20  # the plain copy whose HBM counters calibrate FETCH_SIZE / WRITE_SIZE
+
+
+def attn_roofline(dev, L, W, cap, n_causal=1, copies=ATTN_COPIES, Hq=16, Hkv=2, D=128):
+    """Average duration of one draft (n_causal=1) or verify (None) attention call (gss_draft_attn / gss_verify_attn:
+    split kernel + merge) at prefix L, window W, capacity cap, over ``copies`` distinct random caches in shuffled
+    16-token pages, so the K/V stream comes from HBM as in a round. Returns microseconds per call."""
+    from gravityocr_amd import kernels as K
+    g = torch.Generator(device=dev).manual_seed(1)
+    pages = (cap + 15) // 16
+    kp = torch.randn(copies, pages, Hkv, 16, D, device=dev, generator=g).div_(D ** 0.5).bfloat16()
+    vp = torch.randn(copies, pages, Hkv, D, 16, device=dev, generator=g).div_(D ** 0.5).bfloat16()
+    pt = torch.randperm(pages, device=dev, generator=g).int().view(1, -1)
+    q = torch.randn(1, W, Hq, D, device=dev, generator=g).div_(D ** 0.5).bfloat16()
+    kw = torch.randn(1, W, Hkv, D, device=dev, generator=g).div_(D ** 0.5).bfloat16()
+    vw = torch.randn_like(kw)
+    o = torch.empty_like(q)
+    sl = torch.tensor([L], dtype=torch.int32, device=dev)
+    ws = torch.zeros(max(1, K.attn_workspace_bytes(1, Hq, Hkv, D, W, cap)), dtype=torch.uint8, device=dev)
+    fns = [lambda i=i: K.window_attention(q, kp[i], vp[i], pt, sl, kw, vw, o, n_causal=n_causal, scale=D ** -0.5,
+                                          max_kv_len=cap, workspace=ws) for i in range(copies)]
+    return time_kernel(fns, n=2)
+
+
+def copy_calibration(dev, reps=3):
+    """Plain device copies of COPY_BYTES, as an elementwise kernel (reads COPY_BYTES, writes COPY_BYTES): the
+    calibration kernel of the FETCH_SIZE / WRITE_SIZE passes."""
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+
+
+def traffic_from_profile():
+    """HBM bytes per draft-attention call from the committed counter summary (two rocprofv3 --pmc passes,
+    FETCH_SIZE then WRITE_SIZE, scaled by the copy calibration), or None when it is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "attn_draft_bs1_8k_counters.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_call:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def time_kernel(fn, n=100, reps=5):
-    """average duration of one fn() launch: n launches captured back to back in one HIP graph (no host work between
-    them), replayed ``reps`` times between HIP events on the capture/launch stream; returns microseconds."""
-    fn()
+    """average duration of one launch of fn (a callable, or a list of callables launched in turn): n passes captured
+    back to back in one HIP graph (no host work between them), replayed ``reps`` times between HIP events on the
+    capture/launch stream; returns microseconds."""
+    fns = fn if isinstance(fn, (list, tuple)) else [fn]
+    for f in fns:
+        f()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for _ in range(n):
-            fn()
+            for f in fns:
+                f()
     g.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -58,7 +112,7 @@ def time_kernel(fn, n=100, reps=5):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / (n * reps)  # us
+    return e0.elapsed_time(e1) * 1e3 / (n * reps * len(fns))  # us
 
 
 def main():
@@ -72,11 +126,25 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--profile-only", action="store_true", help="skip AR, planted and CPU legs (for rocprof runs)")
+    ap.add_argument("--attn-only", action="store_true",
+                    help="only the draft-attention roofline measurement and the copy calibration (for rocprof runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the self-spec round shards by sequence (no collective), so a multi-GPU "
               "figure is N independent copies of this one; run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    if args.attn_only:
+        dev = torch.device("cuda:0")
+        L, Kw = args.prefix + args.tokens // 2, args.bd + 1
+        cap = args.prefix + args.tokens + 4 * (Kw + 1) + 64
+        d_us = attn_roofline(dev, L, Kw, cap)
+        copy_calibration(dev)
+        ab = attn_bytes(L, Kw)
+        print(json.dumps({"kernel": "gss_draft_attn", "L": L, "W": Kw, "avg_us": round(d_us, 2),
+                          "algorithmic_bytes": ab, "achieved_GBs": round(ab / (d_us * 1e-6) / 1e9, 1),
+                          "copy_bytes": COPY_BYTES}), flush=True)
+        return
 
     from gravityocr_amd.engine import GssEngine, SelfSpecDecoder
     from gravityocr_amd.model import SYNTH_1536 as cfg, synthetic_prompt, synthetic_weights
@@ -217,19 +285,8 @@ def main():
 
     # ---- draft attention roofline at the round's shape -----------------------------------------------------------
     L = P + args.tokens // 2
-    b = dec.draft_b
-    sl = torch.tensor([L], dtype=torch.int32, device=dev)
-
-    def draft_attn():
-        K.window_attention(b.q, eng.k_pages[0], eng.v_pages[0], eng.page_table[:1], sl, b.k_win[0], b.v_win[0], b.o,
-                           n_causal=1, scale=eng.scale, max_kv_len=eng.max_len, workspace=eng.ws_attn)
-
-    def verify_attn():
-        K.window_attention(b.q, eng.k_pages[0], eng.v_pages[0], eng.page_table[:1], sl, b.k_win[0], b.v_win[0], b.o,
-                           n_causal=None, scale=eng.scale, max_kv_len=eng.max_len, workspace=eng.ws_attn)
-
-    d_us = time_kernel(draft_attn)
-    v_us = time_kernel(verify_attn)
+    d_us = attn_roofline(dev, L, Kw, eng.max_len)
+    v_us = attn_roofline(dev, L, Kw, eng.max_len, n_causal=None)
     ab = attn_bytes(L, Kw)
     achieved = ab / (d_us * 1e-6) / 1e9
     tflops = attn_flops(L, Kw) / (d_us * 1e-6) / 1e12
@@ -289,7 +346,7 @@ def main():
         "prefill_s": round(prefill_s, 2),
         "roofline": {"bound": "hbm", "kernel": "gss_draft_attn (block-diffusion draft attention)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
                      "algorithmic_bytes": ab, "avg_us": round(d_us, 2), "L": L, "W": Kw,
                      "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "verify_avg_us": round(v_us, 2)},

@@ -3,8 +3,9 @@
 //
 // Grid (n_layers, bs); each workgroup copies one layer of one sequence: n_b rows x Hkv heads x D dims of K
 // (16-byte stores into [page][head][token][D]) and of V (token-minor pages [page][head][D][16], 2-byte stores).
-// The committed length of sequence b is read by all n_layers workgroups and advanced by the last of them
-// (agent-scope release/acquire around a counter in the workspace, reset afterwards).
+// The committed length of sequence b is read by all n_layers workgroups and advanced by the last of them to count
+// itself in (agent-scope atomic counter in the workspace, after every workgroup has read the length; reset
+// afterwards).
 #include "gss_common.h"
 
 namespace {

@@ -332,7 +332,8 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
         if ((f * NT + n) % NW == wv && live(f, n)) epilogue(f, n, reduced(f, n));
   } else {
     // this split's partial tile -> workspace; the last split of the column tile to arrive sums all splits in split
-    // order (agent-scope release / acquire around the counter) and runs the epilogue, then resets the counter
+    // order and runs the epilogue, then resets the counter. Partials are agent-scope stores (written through to the
+    // coherence point), waited for before the barrier and the counter bump; the last reads them with agent loads.
     auto part_at = [&](int k, int f, int n) {
       return reinterpret_cast<uint64_t*>(p.part + (static_cast<int64_t>(k) * p.M + n * 16 + l16) * p.N + f0 +
                                          f * 16 + g4 * 4);
