@@ -301,8 +301,13 @@ class RoundState:
 class SelfSpecDecoder:
     """The full-draft self-spec round and the AR step over a GssEngine, device resident and graph-capturable."""
 
-    def __init__(self, eng: GssEngine, bd: int, mask_id: int, bs: int = 1, max_rounds: int = 4096):
+    def __init__(self, eng: GssEngine, bd: int, mask_id: int, bs: int = 1, max_rounds: int = 4096,
+                 softmax_rule: bool = False):
         self.eng, self.bd, self.mask_id, self.bs = eng, bd, mask_id, bs
+        # greedy rule for rows holding a NaN or +inf: the serving worker's raw argmax (NaN as the maximum), or the
+        # HF path's argmax of the fp32 softmax (index 0) with the raw bonus row (src/fast_sampling.py:572-575)
+        self.f_draft = K.ARGMAX_SOFTMAX if softmax_rule else 0
+        self.f_verify = (K.ARGMAX_SOFTMAX | K.ARGMAX_LAST_RAW) if softmax_rule else 0
         Kw = bd + 1
         dev = eng.device
         i32 = dict(dtype=torch.int32, device=dev)
@@ -334,7 +339,7 @@ class SelfSpecDecoder:
         e, s = self.eng, self.st
         s.win[:, 0].copy_(s.x0)
         lg = e.forward(self.draft_b, ids=s.win, n_causal=1, pos_delta=self.pos_delta)
-        e.argmax(lg, s.am)                                                  # a0, d_1..d_B
+        e.argmax(lg, s.am, flags=self.f_draft)                              # a0, d_1..d_B
         e.commit(self.draft_b, n_add=1)                                     # x0's K/V (causal row 0): S += 1
         if after_draft is not None:
             after_draft()
@@ -349,7 +354,7 @@ class SelfSpecDecoder:
         if self.r0_b is None:
             self.r0_b = e.bufs(self.bs, self.bd)
         lg = e.forward(self.r0_b, ids=self.r0_ids, n_causal=0, pos_delta=self.pos_delta)
-        e.argmax(lg, self.r0_am)
+        e.argmax(lg, self.r0_am, flags=self.f_draft)
         s.am[:, 0].copy_(s.x0)
         s.am[:, 1:].copy_(self.r0_am)
         self._verify()
@@ -357,7 +362,7 @@ class SelfSpecDecoder:
     def _verify(self):
         e, s = self.eng, self.st
         lg = e.forward(self.verify_b, ids=s.am, n_causal=None, pos_delta=self.pos_delta)
-        e.argmax(lg, s.tgt, window=s.am, accept_len=s.acc, next_x0=s.x0, packed=s.packed)
+        e.argmax(lg, s.tgt, window=s.am, accept_len=s.acc, next_x0=s.x0, packed=s.packed, flags=self.f_verify)
         e.commit(self.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)       # a0, d_1..d_acc: S += acc + 1
         # the log index is clamped on the device, so rounds beyond the log's capacity rewrite its last row
         li = s.ctr.clamp(max=s.log.shape[0] - 1)

@@ -30,30 +30,40 @@ from typing import Dict, List, Optional, Tuple
 import torch
 
 from . import kernels as K
+from .diffusion import BlockDiffusionDecoder
 from .engine import PAGE, GssEngine, SelfSpecDecoder
 from .model import config_from_model, weights_from_model
 
-__all__ = ["generate_speculative_natcache", "teacher_force_argmax", "enable_fused_flex", "prepare_prompt"]
+__all__ = ["generate_speculative_natcache", "generate_cached", "teacher_force_argmax", "enable_fused_flex",
+           "prepare_prompt"]
 
 _MIN_CAPACITY = 4096
 
 
 class _Session:
-    """One model's decoder weights on the GPU, a paged KV pool for one sequence and its round decoders."""
+    """One model's decoder weights on the GPU, a paged KV pool for ``max_bs`` sequences and its decoders."""
 
-    def __init__(self, model, device: torch.device, capacity: int):
+    def __init__(self, model, device: torch.device, capacity: int, max_bs: int = 1):
         self.cfg = config_from_model(model)
-        self.capacity = capacity
-        self.eng = GssEngine(self.cfg, weights_from_model(model), max_bs=1, max_len=capacity, device=device)
+        self.capacity, self.max_bs = capacity, max_bs
+        self.eng = GssEngine(self.cfg, weights_from_model(model), max_bs=max_bs, max_len=capacity, device=device)
         self.decoders: Dict[Tuple[int, int], SelfSpecDecoder] = {}
         self.graphed: Dict[Tuple[int, int], bool] = {}
+        self.diffusion: Dict[tuple, BlockDiffusionDecoder] = {}
+
+    def diffusion_decoder(self, bs: int, bd: int, mask_id: int, threshold: float,
+                          commit_causal: bool) -> BlockDiffusionDecoder:
+        key = (bs, bd, mask_id, float(threshold), bool(commit_causal))
+        if key not in self.diffusion:
+            self.diffusion[key] = BlockDiffusionDecoder(self.eng, bd, mask_id, bs, threshold, commit_causal)
+        return self.diffusion[key]
 
     def decoder(self, bd: int, mask_id: int) -> SelfSpecDecoder:
         key = (bd, mask_id)
         if key not in self.decoders:
             # every round commits at least 2 tokens and writes one log row
             self.decoders[key] = SelfSpecDecoder(self.eng, bd=bd, mask_id=mask_id, bs=1,
-                                                 max_rounds=self.capacity // 2 + 8)
+                                                 max_rounds=self.capacity // 2 + 8, softmax_rule=True)
             self.graphed[key] = False
         return self.decoders[key]
 
@@ -61,12 +71,12 @@ class _Session:
 _SESSIONS: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
 
 
-def _session(model, device: torch.device, need: int) -> _Session:
+def _session(model, device: torch.device, need: int, bs: int = 1) -> _Session:
     s = _SESSIONS.get(model)
-    if s is None or s.capacity < need or s.eng.device != device:
-        cap = max(_MIN_CAPACITY, need)
+    if s is None or s.capacity < need or s.max_bs < bs or s.eng.device != device:
+        cap = max(_MIN_CAPACITY, need, 0 if s is None else s.capacity)
         cap = (cap + 1023) // 1024 * 1024
-        s = _Session(model, device, cap)
+        s = _Session(model, device, cap, max(bs, 1 if s is None else s.max_bs))
         _SESSIONS[model] = s
     return s
 
@@ -116,16 +126,17 @@ def prepare_prompt(model, image, prompt: str, max_long_side: int, device: torch.
     return input_ids, e[0], positions, next_pos
 
 
-def _prefill(eng: GssEngine, emb, positions, logits_rows=None):
-    """Prefill slot 0; 1-D positions (all three M-RoPE rows equal to 0..P-1) take the plain RoPE path."""
+def _prefill(eng: GssEngine, emb, positions, logits_rows=None, slot: int = 0):
+    """Prefill one slot; 1-D positions (all three M-RoPE rows equal to 0..P-1) take the plain RoPE path."""
     P = emb.shape[0]
     ar = torch.arange(P, dtype=torch.int32, device=positions.device)
     plain = bool(((positions == ar[:, None]).all()).item())
-    return eng.prefill(0, emb, positions=None if plain else positions, logits_rows=logits_rows)
+    return eng.prefill(slot, emb, positions=None if plain else positions, logits_rows=logits_rows)
 
 
-def _argmax_rows(eng: GssEngine, logits: torch.Tensor) -> torch.Tensor:
-    """Greedy ids of logits [n, V] (bf16) with the kernel's rule (max value, lowest index on ties, NaN as max)."""
+def _argmax_rows(eng: GssEngine, logits: torch.Tensor, softmax_rule: bool = False) -> torch.Tensor:
+    """Greedy ids of logits [n, V] (bf16): max value, lowest index on ties; a row with a NaN gives the NaN's index
+    (torch.argmax of the logits), or 0 with ``softmax_rule`` (argmax of the fp32 softmax, all NaN)."""
     n = logits.shape[0]
     out = torch.empty(n, 1, dtype=torch.int32, device=logits.device)
     step = 1024                                     # sequences per argmax launch
@@ -133,11 +144,12 @@ def _argmax_rows(eng: GssEngine, logits: torch.Tensor) -> torch.Tensor:
         j = min(n, i + step)
         lg = logits[i:j].contiguous().view(j - i, 1, -1)
         ws = torch.zeros(K.argmax_workspace_bytes(j - i, 1, lg.shape[-1]), dtype=torch.uint8, device=logits.device)
-        K.argmax_accept(lg, out[i:j], ws)
+        K.argmax_accept(lg, out[i:j], ws, flags=K.ARGMAX_SOFTMAX if softmax_rule else 0)
     return out[:, 0]
 
 
 def _check_greedy(temperature, accept_conf=0.0, draft_steps=1, full_draft=True):
+    """Reject the non-greedy and non-default modes this path does not implement (no silent fallback)."""
     if temperature and temperature > 0:
         raise NotImplementedError("only greedy decoding (temperature=0) runs on the MI355X path")
     if accept_conf and accept_conf > 0:
@@ -183,7 +195,7 @@ def generate_speculative_natcache(model, image, prompt="Text Recognition:", max_
         log_rows: List[List[int]] = []
     else:
         seed_logit = _prefill(eng, emb, positions)
-        a0 = _argmax_rows(eng, seed_logit.view(1, -1))
+        a0 = _argmax_rows(eng, seed_logit.view(1, -1), softmax_rule=True)
         dec.start(a0, pos_delta=torch.full((1,), next_pos - P, dtype=torch.int32, device=device))
         log_rows = _run_rounds(sess, dec, key, bd, max_new_tokens, eos_id)
     n_rounds = len(log_rows)
@@ -257,6 +269,71 @@ def _run_rounds(sess: _Session, dec: SelfSpecDecoder, key, bd: int, max_new_toke
             issue()
     torch.cuda.synchronize(device)
     return rows
+
+
+@torch.no_grad()
+def generate_cached(model, image, prompt="Text Recognition:", max_new_tokens=512,
+                    threshold=0.99, temperature=0.0, top_p=0.95, max_long_side=1344, commit_trace=None,
+                    commit_causal=False, commit_detail=None):
+    """KV-cached block-diffusion decode (src/fast_sampling.py:105-258) on the MI355X kernels: blocks of
+    ``model.bd_size`` positions, threshold unmasking against the frozen cache, one commit forward per block.
+
+    Same arguments and return value (the decoded text). ``commit_trace`` receives the number of positions each
+    probe forward unmasked; ``commit_detail`` receives the reference's records (the seed of every block, then per
+    probe forward the unmasked positions, ids and confidences and ``pred_all`` over the masked positions). Greedy
+    only (``temperature == 0``; ``top_p`` is read by the sampling branch alone)."""
+    _check_greedy(temperature)
+    device = _model_device(model)
+    bd, mask_id = int(model.bd_size), int(model.mask_id)
+    eos_id = model.tokenizer.eos_token_id
+    input_ids, emb, positions, next_pos = prepare_prompt(model, image, prompt, max_long_side, device)
+    P = input_ids.shape[1]
+    num_blocks = (max_new_tokens + bd - 1) // bd
+    sess = _session(model, device, P + num_blocks * bd + PAGE)
+    seed = int(_argmax_rows(sess.eng, _prefill(sess.eng, emb, positions).view(1, -1), softmax_rule=True)[0])
+    dec = sess.diffusion_decoder(1, bd, mask_id, threshold, commit_causal)
+    dec.start(torch.tensor([seed]), pos_delta=torch.tensor([next_pos - P]))
+    generated: List[int] = []
+    done = False
+    for blk in range(num_blocks):
+        if done or (eos_id is not None and seed == eos_id):
+            break
+        frozen = P + blk * bd
+        if commit_detail is not None:
+            commit_detail.append({"block": int(frozen // bd), "step": len(commit_detail), "pos": [int(frozen)],
+                                  "in_block_pos": [0], "tok": [int(seed)], "conf": [1.0], "is_seed": True})
+        on_step = None
+        if commit_trace is not None or commit_detail is not None:
+            def on_step(frozen=frozen):
+                _record_step(dec, frozen, bd, mask_id, commit_trace, commit_detail)
+        blocks, seeds, _ = dec.decode_block([seed], on_step)
+        seed = seeds[0]
+        for t in blocks[0]:
+            if eos_id is not None and t == eos_id:
+                done = True
+                break
+            generated.append(t)
+    return _decode_text(model, generated, device)
+
+
+def _record_step(dec: BlockDiffusionDecoder, frozen: int, bd: int, mask_id: int, commit_trace, commit_detail):
+    """commit_trace / commit_detail entries of one probe step of row 0 (src/fast_sampling.py:217-238). A position
+    counts as unmasked when it was masked before the step and holds another id after it."""
+    before, after = dec.before[0].tolist(), dec.block[0].tolist()
+    if commit_trace is not None:
+        commit_trace.append(int(dec.n_unmasked[0]))
+    if commit_detail is None:
+        return
+    idx = [i for i in range(bd) if before[i] == mask_id and after[i] != mask_id]
+    if not idx:
+        return
+    x1, conf = dec.x1[0].tolist(), dec.conf[0].tolist()
+    mp = [i for i in range(bd) if before[i] == mask_id]
+    commit_detail.append({"pred_all": {"pos": mp, "tok": [int(x1[i]) for i in mp],
+                                       "conf": [round(float(conf[i]), 4) for i in mp]},
+                          "block": int(frozen // bd), "step": len(commit_detail),
+                          "pos": [int(frozen + i) for i in idx], "in_block_pos": idx,
+                          "tok": [int(x1[i]) for i in idx], "conf": [round(float(conf[i]), 4) for i in idx]})
 
 
 def _capture_round(dec: SelfSpecDecoder):

@@ -81,9 +81,15 @@ def window_attention(q, k_pages, v_pages, page_table, prefix_len, k_win, v_win, 
     return out
 
 
-def argmax_accept(logits, target, workspace, *, window=None, accept_len=None, next_x0=None, packed=None):
+ARGMAX_SOFTMAX, ARGMAX_LAST_RAW = 1, 2
+
+
+def argmax_accept(logits, target, workspace, *, window=None, accept_len=None, next_x0=None, packed=None,
+                  flags: int = 0):
     """logits [bs, W, V] (bf16 or fp32, rows may be strided: logits.stride(1) is the row stride, last dim dense);
-    target int32 [bs, W]. With ``window`` (int32 [bs, W]) also accept_len / next_x0 [bs] and packed [bs, W+2]."""
+    target int32 [bs, W]. With ``window`` (int32 [bs, W]) also accept_len / next_x0 [bs] and packed [bs, W+2].
+    ``flags``: ARGMAX_SOFTMAX (argmax of the fp32 softmax: rows with a NaN or +inf give 0), optionally with
+    ARGMAX_LAST_RAW (the last row of each sequence keeps the raw rule, NaN as the maximum)."""
     bs, W, V = logits.shape
     if not logits.is_cuda or logits.stride(2) != 1 or logits.stride(0) != W * logits.stride(1):
         raise ValueError("logits must be a GPU tensor [bs, W, V] with dense rows and a uniform row stride")
@@ -98,9 +104,40 @@ def argmax_accept(logits, target, workspace, *, window=None, accept_len=None, ne
     need = argmax_workspace_bytes(bs, W, V)
     if workspace.numel() * workspace.element_size() < need:
         raise ValueError("argmax workspace too small")
-    check(lib().gss_argmax_accept(_ptr(logits), dt, logits.stride(1), bs, W, V, _ptr(window), _ptr(target),
+    check(lib().gss_argmax_accept(_ptr(logits), dt, logits.stride(1), bs, W, V, int(flags), _ptr(window), _ptr(target),
                                   _ptr(accept_len), _ptr(next_x0), _ptr(packed), _ptr(workspace),
                                   workspace.numel() * workspace.element_size(), _stream()), "gss_argmax_accept")
+
+
+def unmask_workspace_bytes(bs, W, V) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().gss_unmask_workspace_size(bs, W, V, ctypes.byref(n)), "gss_unmask_workspace_size")
+    return n.value
+
+
+def unmask_step(logits, block, workspace, *, mask_id: int, threshold: float, x1=None, conf=None, n_unmasked=None,
+                n_left=None, seed=None):
+    """One threshold-unmask step of the block-diffusion decode (gss_unmask_step). logits [bs, W, V] bf16 or fp32
+    (uniform row stride, dense rows); block int32 [bs, W] (updated in place); optional outputs x1 int32 [bs, W],
+    conf float32 [bs, W], n_unmasked / n_left / seed int32 [bs]."""
+    bs, W, V = logits.shape
+    if not logits.is_cuda or logits.stride(2) != 1 or logits.stride(0) != W * logits.stride(1):
+        raise ValueError("logits must be a GPU tensor [bs, W, V] with dense rows and a uniform row stride")
+    dt = {torch.bfloat16: 0, torch.float32: 1}.get(logits.dtype)
+    if dt is None:
+        raise ValueError("logits must be bf16 or fp32")
+    _need(block, torch.int32, "block", (bs, W))
+    for name, t, dtype, shp in (("x1", x1, torch.int32, (bs, W)), ("conf", conf, torch.float32, (bs, W)),
+                                ("n_unmasked", n_unmasked, torch.int32, (bs,)), ("n_left", n_left, torch.int32, (bs,)),
+                                ("seed", seed, torch.int32, (bs,))):
+        if t is not None:
+            _need(t, dtype, name, shp)
+    if workspace.numel() * workspace.element_size() < unmask_workspace_bytes(bs, W, V):
+        raise ValueError("unmask workspace too small")
+    check(lib().gss_unmask_step(_ptr(logits), dt, logits.stride(1), bs, W, V, _ptr(block), int(mask_id),
+                                float(threshold), _ptr(x1), _ptr(conf), _ptr(n_unmasked), _ptr(n_left), _ptr(seed),
+                                _ptr(workspace), workspace.numel() * workspace.element_size(), _stream()),
+          "gss_unmask_step")
 
 
 def kv_commit(k_win, v_win, k_pages, v_pages, page_table, seq_lens, workspace, *, n_rows=None, n_add=0,

@@ -163,9 +163,12 @@ class _Processor:
 
     def __call__(self, text=None, images=None, return_tensors="pt"):
         o = self.owner
-        ids = torch.cat([torch.full((o.n_vis,), o.image_token_id, dtype=torch.long), o.prompt_ids])[None]
-        return _Enc(input_ids=ids, mm_token_type_ids=torch.zeros_like(ids), pixel_values=torch.zeros(1),
-                    image_grid_thw=torch.tensor([[1, 1, o.n_vis]]))
+        key = o.crop_key(images[0] if images else None)
+        vis, prompt_ids = o.crop(key)
+        n_vis = vis.shape[0]
+        ids = torch.cat([torch.full((n_vis,), o.image_token_id, dtype=torch.long), prompt_ids])[None]
+        return _Enc(input_ids=ids, mm_token_type_ids=torch.zeros_like(ids), pixel_values=torch.tensor([key]),
+                    image_grid_thw=torch.tensor([[1, 1, n_vis]]))
 
 
 class _Tokenizer:
@@ -185,7 +188,7 @@ class _MM:
         class _R:
             pass
         r = _R()
-        r.pooler_output = [self.owner.visual]
+        r.pooler_output = [self.owner.crop(int(pixel_values.reshape(-1)[0]))[0]]
         return r
 
     def get_rope_index(self, input_ids, mm_tt, image_grid_thw=None, video_grid_thw=None, attention_mask=None):
@@ -195,7 +198,9 @@ class _MM:
 
 class SyntheticGlmOcr(torch.nn.Module):
     """Random-init GLM-OCR stand-in: the decoder above, a synthetic 'image' (n_vis N(0,1) embeddings) and a fixed
-    prompt of token ids. Positions are 1-D (the three M-RoPE rows equal)."""
+    prompt of token ids. Positions are 1-D (the three M-RoPE rows equal). More crops, each with its own embeddings
+    and prompt ids, can be added with ``add_crop``: a PIL image whose width is a crop's key encodes as that crop,
+    any other image as the default one."""
 
     def __init__(self, cfg: GlmTextConfig, weights, visual, prompt_ids, mask_id, bd_size, eos_id=None,
                  image_token_id=None, dtype=torch.float32):
@@ -218,6 +223,25 @@ class SyntheticGlmOcr(torch.nn.Module):
         self.mm_model = _MM(self)
         self.processor = _Processor(self)
         self.tokenizer = _Tokenizer(eos_id)
+        self._dtype = dtype
+        self.crops = {}
+
+    def add_crop(self, key: int, visual: torch.Tensor, prompt_ids: torch.Tensor):
+        """Register a crop for images of width ``key`` (> 0)."""
+        if key <= 0:
+            raise ValueError("crop keys are image widths > 0")
+        self.crops[int(key)] = (visual.to(self._dtype), prompt_ids.long())
+
+    def crop_key(self, image) -> int:
+        w = getattr(image, "size", (0,))[0] if image is not None else 0
+        return int(w) if int(w) in self.crops else 0
+
+    def crop(self, key: int):
+        """(visual embeddings, prompt ids) of crop ``key`` (0 = the default crop)."""
+        if key in self.crops:
+            vis, ids = self.crops[key]
+            return vis.to(self.visual.device), ids
+        return self.visual, self.prompt_ids
 
     def _sample_top_p(self, logits, top_p, temperature):
         logits = logits.float()

@@ -38,6 +38,17 @@ enum gss_status {
 
 enum gss_dtype { GSS_BF16 = 0, GSS_F32 = 1 };
 
+/* argmax rule flags (gss_argmax_accept) */
+enum gss_argmax_flags {
+  /* argmax(softmax(float(logits))) as src/models/glm_ocr_dllm.py:997-1002 computes it: a row holding a NaN or +inf
+   * has an all-NaN fp32 softmax, whose argmax is 0. Without the flag a NaN counts as the maximum (torch.argmax on
+   * the raw logits, the serving worker's rule: selfspec_diffusion_worker.py:742). */
+  GSS_ARGMAX_SOFTMAX = 1,
+  /* with GSS_ARGMAX_SOFTMAX: the last row of each sequence keeps the raw rule (natcache's verify takes ar_pred from
+   * the softmax and the bonus from the raw logits of the last row, src/fast_sampling.py:572-575) */
+  GSS_ARGMAX_LAST_RAW = 2
+};
+
 const char* gss_version(void);
 const char* gss_status_string(int status);
 
@@ -81,7 +92,8 @@ int gss_verify_attn(const void* q, const void* k_pages, const void* v_pages, con
  * :574-575) and sgl-kernel verify_tree_greedy on the worker's linear chain (selfspec_fast_commit.py:150-160,
  * chain layout selfspec_diffusion_worker.py:530-548).
  *
- * target[b, r] = argmax of logits row (b, r), r in [0, W).
+ * target[b, r] = argmax of logits row (b, r), r in [0, W): the maximum, the lowest index on ties; flags selects
+ * the rule for rows with a NaN or +inf (gss_argmax_flags).
  * With window != NULL (the verify ids [a0, d_1..d_{W-1}] of each sequence) also:
  *   accept_len[b] = number of leading r in [0, W-2] with target[b, r] == window[b, r+1]
  *   next_x0[b]    = target[b, accept_len[b]]              (the correction, or the bonus when all W-1 matched)
@@ -92,9 +104,30 @@ int gss_verify_attn(const void* q, const void* k_pages, const void* v_pages, con
  */
 int gss_argmax_workspace_size(int bs, int W, int V, size_t* bytes);
 
-int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, int bs, int W, int V, const int32_t* window,
-                      int32_t* target, int32_t* accept_len, int32_t* next_x0, int32_t* packed, void* workspace,
-                      size_t workspace_bytes, gss_stream_t stream);
+int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, int bs, int W, int V, int flags,
+                      const int32_t* window, int32_t* target, int32_t* accept_len, int32_t* next_x0, int32_t* packed,
+                      void* workspace, size_t workspace_bytes, gss_stream_t stream);
+
+/* ---------------------------------------------------------------- block-diffusion unmask step -------------------
+ * Replaces one iteration of the threshold-unmask loop of the cached block-diffusion decode at temperature 0
+ * (src/fast_sampling.py:206-216 generate_cached; src/fast_sampling_batched.py:198-211 generate_cached_batched):
+ *   logits  = lm_head rows of the block forward, [bs, W, V] (row stride ld_row)
+ *   shifted = in-block token shift: position j reads row max(j - 1, 0)
+ *   x1[j]   = argmax of softmax(float(shifted[j])) (GSS_ARGMAX_SOFTMAX rule), conf[j] = its probability
+ *   unmask  = masked positions (block == mask_id) with conf > threshold, plus the first position of the largest
+ *             conf among the masked ones (NaN as the largest); block[j] = x1[j] where unmasked.
+ * Outputs (each may be NULL): x1 and conf [bs, W] (every position, masked or not), n_unmasked[b] (positions the rule
+ * unmasked), n_left[b] (positions holding mask_id afterwards), seed[b] = argmax of row W - 1 without shift (the next block's seed after the commit forward,
+ * src/fast_sampling.py:187-190). A block without masks is left unchanged. conf is 1 / sum(exp(x - max)), summed in
+ * a fixed order (within a few ulp of torch's softmax).
+ * Workspace: gss_unmask_workspace_size bytes, zeroed once after allocation (the first 4 KiB are per-sequence
+ * counters, the same layout as the argmax workspace).
+ */
+int gss_unmask_workspace_size(int bs, int W, int V, size_t* bytes);
+
+int gss_unmask_step(const void* logits, int dtype, int64_t ld_row, int bs, int W, int V, int32_t* block, int mask_id,
+                    float threshold, int32_t* x1, float* conf, int32_t* n_unmasked, int32_t* n_left, int32_t* seed,
+                    void* workspace, size_t workspace_bytes, gss_stream_t stream);
 
 /* ---------------------------------------------------------------- (d) KV commit ---------------------------------
  * Replaces the commit half of _ss_commit_kernel (selfspec_fast_commit.py:139-147: seq_lens += acc + 1, rejected

@@ -18,4 +18,7 @@ Pinning (what each function is checked against, in ``tests/``):
   decoder layer       transformers' GlmOcrTextDecoderLayer (container copy, third party) on the same weights
   natcache / fulldraft rounds   golden traces written by importing the reference's generate_speculative_natcache
                       (tests/golden/make_golden.py) + AR-equivalence (committed ids == greedy AR ids)
+  block diffusion     golden ids / commit traces / commit details written by importing the reference's
+                      generate_cached and generate_cached_batched (tests/golden/make_golden_diffusion.py); the
+                      unmask rule against a brute-force fp64 reading (tests/test_oracle_diffusion.py)
 """

@@ -44,6 +44,10 @@ def test_host_side_queries_and_status_strings():
     assert L.gss_attn_workspace_size(1, 16, 3, 128, 17, 8192, ctypes.byref(n)) == UNSUPPORTED   # Hq % Hkv
     assert L.gss_attn_workspace_size(1, 16, 2, 96, 17, 8192, ctypes.byref(n)) == UNSUPPORTED    # head dim
     assert L.gss_kv_commit_workspace_size(4, ctypes.byref(n)) == OK
+    # unmask: counters (4 KiB) + chunk (max, sum, index) of ceil(V / 4096) chunks per row
+    assert L.gss_unmask_workspace_size(2, 32, 59392, ctypes.byref(n)) == OK
+    assert n.value == 4096 + 2 * 32 * 15 * 12
+    assert L.gss_unmask_workspace_size(1, 65, 100, ctypes.byref(n)) == UNSUPPORTED
 
 
 def test_entry_points_reject_bad_arguments_before_launch():
@@ -52,7 +56,8 @@ def test_entry_points_reject_bad_arguments_before_launch():
     # null pointers
     assert L.gss_draft_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 17, 1, 16, 2, 128, 16, 0.1,
                             8192, null, 0, null) == ARG
-    assert L.gss_argmax_accept(null, 0, 100, 1, 1, 100, null, null, null, null, null, null, 0, null) == ARG
+    assert L.gss_argmax_accept(null, 0, 100, 1, 1, 100, 0, null, null, null, null, null, null, 0, null) == ARG
+    assert L.gss_unmask_step(null, 0, 100, 1, 4, 100, null, 7, 0.9, null, null, null, null, null, null, 0, null) == ARG
     # unsupported page size / window wider than a tile: rejected before pointers are looked at
     assert L.gss_verify_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 17, 16, 2, 128, 32, 0.1,
                              8192, null, 0, null) == UNSUPPORTED
@@ -76,13 +81,25 @@ REFERENCE_SIGNATURES = {
                              ("max_long_side", 1344)],
     # src/fast_sampling.py:50
     "enable_fused_flex": [("dynamic", True)],
+    # src/fast_sampling.py:105-107
+    "generate_cached": [
+        ("model", inspect.Parameter.empty), ("image", inspect.Parameter.empty), ("prompt", "Text Recognition:"),
+        ("max_new_tokens", 512), ("threshold", 0.99), ("temperature", 0.0), ("top_p", 0.95),
+        ("max_long_side", 1344), ("commit_trace", None), ("commit_causal", False), ("commit_detail", None)],
+    # src/fast_sampling_batched.py:95-97
+    "fast_sampling_batched.generate_cached_batched": [
+        ("model", inspect.Parameter.empty), ("images", inspect.Parameter.empty), ("prompt", "Text Recognition:"),
+        ("max_new_tokens", 512), ("threshold", 0.99), ("temperature", 0.0), ("top_p", 0.95),
+        ("max_long_side", 1344)],
 }
 
 
 @pytest.mark.parametrize("name", sorted(REFERENCE_SIGNATURES))
 def test_dropin_signatures_match_reference(name):
-    from gravityocr_amd import fast_sampling
-    params = inspect.signature(getattr(fast_sampling, name)).parameters
+    import importlib
+    mod, _, fn = name.rpartition(".")
+    module = importlib.import_module("gravityocr_amd." + (mod or "fast_sampling"))
+    params = inspect.signature(getattr(module, fn)).parameters
     assert [(p.name, p.default) for p in params.values()] == REFERENCE_SIGNATURES[name]
 
 
@@ -96,6 +113,14 @@ def test_dropin_rejects_unimplemented_modes_and_cpu_models():
             generate_speculative_natcache(m, None, **kw)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         generate_speculative_natcache(m, None)
+    from gravityocr_amd.fast_sampling import generate_cached
+    from gravityocr_amd.fast_sampling_batched import generate_cached_batched
+    with pytest.raises(NotImplementedError):
+        generate_cached(m, None, temperature=0.5)
+    with pytest.raises(NotImplementedError):
+        generate_cached_batched(m, [None], temperature=0.5)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        generate_cached(m, None)
 
 
 def test_gemm_workspace_sizes_follow_the_k_split():
