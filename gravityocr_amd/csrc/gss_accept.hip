@@ -3,8 +3,8 @@
 // Phase 1: workgroup (chunk, row) scans 4096 logits of one row (16 per thread, 16-byte loads), keeps the best
 //   (value, index) under the greedy rule (max value, lowest index on ties, NaN as max), reduces across the
 //   wavefront with xor-shuffles and across the workgroup through LDS, and stores the chunk's winner.
-// Phase 2: the last workgroup to finish for a sequence (chunk winners handed over through the coherence point and an
-//   atomic counter in the workspace) reduces the chunk winners of each of its W rows in chunk order, then runs the linear-chain accept:
+// Phase 2: the last workgroup to finish for a sequence (chunk winners handed over through the coherence point and
+//   two levels of atomic counters in the workspace) reduces the chunk winners of each of its W rows in chunk order, then runs the linear-chain accept:
 //   acc = leading r with target[r] == window[r+1]; next_x0 = target[acc]; packed row as the reference's readback.
 //   It then resets the counter, so the workspace needs zeroing only once and the launch is graph-replayable.
 #include "gss_common.h"
@@ -15,6 +15,7 @@ constexpr int ARG_THREADS = 256;
 constexpr int PER_THREAD = 16;
 constexpr int CHUNK = ARG_THREADS * PER_THREAD;  // logits per workgroup
 constexpr int MAX_W = 64;
+constexpr int MAX_CHUNKS = 32;  // V <= MAX_CHUNKS * CHUNK (131072)
 
 struct Best {
   float v;
@@ -80,6 +81,30 @@ GSS_DEV void scan16(const T* row, int j0, int V, float& bv, int& bi) {
   }
 }
 
+// Arrival counting of the (chunk, row) workgroups of one sequence, in two levels: workgroup g counts into sub-counter
+// g % SUB, the last arrival of each sub-counter counts into the sequence counter, and the last of those finishes the
+// sequence. Every counter sits on its own 128-byte line: atomics on one line serialize, and a single counter taking
+// W * n_chunks arrivals costs several microseconds. The sub-counters reset themselves; the finishing workgroup resets
+// the sequence counter when it is done.
+constexpr int SUB = 8;
+constexpr int LINE_U32 = 32;
+constexpr int MAX_SEQ = 1024;
+constexpr size_t COUNTER_BYTES = static_cast<size_t>(MAX_SEQ) * (SUB + 1) * LINE_U32 * sizeof(uint32_t);
+
+GSS_DEV uint32_t* seq_counter(uint32_t* counters, int b) {
+  return counters + static_cast<size_t>(b) * (SUB + 1) * LINE_U32;
+}
+
+GSS_DEV bool arrive_last(uint32_t* counters, int b, int g, int n_g) {
+  uint32_t* base = seq_counter(counters, b);
+  const int sub = g % SUB;
+  const int in_sub = (n_g - 1 - sub) / SUB + 1;  // workgroups counting into this sub-counter
+  uint32_t* c = base + (1 + sub) * LINE_U32;
+  if (count_arrival(c) != static_cast<uint32_t>(in_sub - 1)) return false;
+  reset_counter(c);
+  return count_arrival(base) == static_cast<uint32_t>((n_g < SUB ? n_g : SUB) - 1);
+}
+
 struct ArgParams {
   const void* logits;
   int64_t ld_row;
@@ -89,10 +114,10 @@ struct ArgParams {
   int32_t* accept_len;
   int32_t* next_x0;
   int32_t* packed;
-  float* part_v;       // [bs*W, n_chunks]
-  int32_t* part_i;     // [bs*W, n_chunks]
-  uint32_t* counters;  // [bs]
+  uint64_t* part;      // [bs*W, n_chunks] chunk winner (value bits | index << 32)
+  uint32_t* counters;  // arrival counters (see arrive_last)
 };
+
 
 template <typename T>
 __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p) {
@@ -120,27 +145,38 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
     for (int w = 1; w < ARG_THREADS / 64; ++w)
       if (beats(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
     const int64_t slot = static_cast<int64_t>(row) * p.n_chunks + chunk;
-    st_agent(reinterpret_cast<uint32_t*>(p.part_v + slot), __float_as_uint(bv));
-    st_agent(reinterpret_cast<uint32_t*>(p.part_i + slot), static_cast<uint32_t>(bi));
+    st_agent(p.part + slot, static_cast<uint64_t>(__float_as_uint(bv)) | (static_cast<uint64_t>(bi) << 32));
     wait_stores();
-    is_last = count_arrival(&p.counters[b]) == static_cast<uint32_t>(p.n_chunks * p.W - 1);
+    const int r = row - b * p.W;
+    is_last = arrive_last(p.counters, b, r * p.n_chunks + chunk, p.W * p.n_chunks);
   }
   __syncthreads();
   if (!is_last) return;
 
   // ---- phase 2: this workgroup finishes sequence b ------------------------------------------------------------
+  // the chunk winners of its W rows, one (row, chunk) per thread (coherent loads), then each row in chunk order
+  __shared__ float cv_s[MAX_W * MAX_CHUNKS];
+  __shared__ int ci_s[MAX_W * MAX_CHUNKS];
   __shared__ int tgt[MAX_W];
-  if (tid < p.W) {
-    const int64_t base = (static_cast<int64_t>(b) * p.W + tid) * p.n_chunks;
-    const uint32_t* pv = reinterpret_cast<const uint32_t*>(p.part_v) + base;
-    const uint32_t* pi = reinterpret_cast<const uint32_t*>(p.part_i) + base;
-    float v = __uint_as_float(ld_agent(pv));
-    int i = static_cast<int>(ld_agent(pi));
-    for (int c = 1; c < p.n_chunks; ++c) {
-      const float cv = __uint_as_float(ld_agent(pv + c));
-      const int ci = static_cast<int>(ld_agent(pi + c));
-      if (beats(cv, ci, v, i)) { v = cv; i = ci; }
+  __shared__ int win_s[MAX_W];
+  if (p.window != nullptr && tid < p.W) win_s[tid] = p.window[static_cast<int64_t>(b) * p.W + tid];
+  {
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(p.part + static_cast<int64_t>(b) * p.W * p.n_chunks);
+    for (int t = tid; t < p.W * p.n_chunks; t += ARG_THREADS) {
+      uint32_t v, i, unused;
+      ld_agent_u32(2, base + 2 * t, base + 2 * t + 1, nullptr, v, i, unused);
+      cv_s[t] = __uint_as_float(v);
+      ci_s[t] = static_cast<int>(i);
     }
+  }
+  __syncthreads();
+  if (tid < p.W) {
+    const float* rv = cv_s + tid * p.n_chunks;
+    const int* ri = ci_s + tid * p.n_chunks;
+    float v = rv[0];
+    int i = ri[0];
+    for (int c = 1; c < p.n_chunks; ++c)
+      if (beats(rv[c], ri[c], v, i)) { v = rv[c]; i = ri[c]; }
     // softmax rule: a NaN or +inf anywhere in the row makes every fp32 softmax probability NaN, whose argmax is 0
     const bool soft = (p.flags & GSS_ARGMAX_SOFTMAX) && !((p.flags & GSS_ARGMAX_LAST_RAW) && tid == p.W - 1);
     if (soft && (v != v || v == INFINITY)) i = 0;
@@ -148,42 +184,41 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
     p.target[b * p.W + tid] = i;
   }
   __syncthreads();
-  if (p.window != nullptr) {
-    __shared__ int acc_s;
+  if (p.window != nullptr && tid < 64) {
+    // accept length = the first r < W-1 with target[r] != window[r+1] (W-1 when every one matches): a ballot over
+    // the lanes of wave 0 instead of a serial scan
+    const bool miss = tid < p.W - 1 && tgt[tid] != win_s[tid + 1];
+    const uint64_t m = __ballot(miss);
+    const int a = m ? __builtin_ctzll(m) : p.W - 1;
     if (tid == 0) {
-      const int32_t* win = p.window + static_cast<int64_t>(b) * p.W;
-      int a = 0;
-      while (a < p.W - 1 && tgt[a] == win[a + 1]) ++a;
-      acc_s = a;
       if (p.accept_len) p.accept_len[b] = a;
       if (p.next_x0) p.next_x0[b] = tgt[a];
       if (p.packed) {
-        p.packed[static_cast<int64_t>(b) * (p.W + 2) + 0] = win[0];
+        p.packed[static_cast<int64_t>(b) * (p.W + 2) + 0] = win_s[0];
         p.packed[static_cast<int64_t>(b) * (p.W + 2) + 1] = a;
       }
     }
-    __syncthreads();
     if (p.packed && tid < p.W)
-      p.packed[static_cast<int64_t>(b) * (p.W + 2) + 2 + tid] = tid <= acc_s ? tgt[tid] : 0;
+      p.packed[static_cast<int64_t>(b) * (p.W + 2) + 2 + tid] = tid <= a ? tgt[tid] : 0;
   }
-  if (tid == 0) reset_counter(&p.counters[b]);
+  if (tid == 0) reset_counter(seq_counter(p.counters, b));
 }
 
-// Workspace layout: the per-sequence counters first (a fixed offset, whatever W and V are, so calls with different
-// window sizes can share one workspace), then the chunk winners' values and indices.
-constexpr size_t COUNTER_BYTES = 4096;  // up to 1024 sequences
+// Workspace layout: the arrival counters first (a fixed block, whatever bs, W and V are, so calls of different shapes
+// can share one workspace), then the chunk winners.
+constexpr size_t PARTS_OFFSET = COUNTER_BYTES;
 
 size_t ws_bytes(int bs, int W, int V) {
   const size_t nc = (static_cast<size_t>(V) + CHUNK - 1) / CHUNK;
   const size_t parts = static_cast<size_t>(bs) * W * nc;
-  return COUNTER_BYTES + parts * (sizeof(float) + sizeof(int32_t));
+  return PARTS_OFFSET + parts * sizeof(uint64_t);
 }
 
 }  // namespace
 
 extern "C" int gss_argmax_workspace_size(int bs, int W, int V, size_t* bytes) {
   if (!bytes || bs <= 0 || W <= 0 || V <= 0) return GSS_ERR_ARG;
-  if (W > MAX_W) return GSS_ERR_UNSUPPORTED;
+  if (W > MAX_W || V > MAX_CHUNKS * CHUNK) return GSS_ERR_UNSUPPORTED;
   *bytes = ws_bytes(bs, W, V);
   return GSS_OK;
 }
@@ -194,7 +229,7 @@ extern "C" int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, 
   if (!logits || !target || bs <= 0 || W <= 0 || V <= 0 || ld_row < V) return GSS_ERR_ARG;
   if (dtype != GSS_BF16 && dtype != GSS_F32) return GSS_ERR_ARG;
   if (flags & ~(GSS_ARGMAX_SOFTMAX | GSS_ARGMAX_LAST_RAW)) return GSS_ERR_ARG;
-  if (W > MAX_W || bs > static_cast<int>(COUNTER_BYTES / sizeof(uint32_t))) return GSS_ERR_UNSUPPORTED;
+  if (W > MAX_W || V > MAX_CHUNKS * CHUNK || bs > MAX_SEQ) return GSS_ERR_UNSUPPORTED;
   if (!workspace || workspace_bytes < ws_bytes(bs, W, V)) return GSS_ERR_WORKSPACE;
   ArgParams p;
   p.logits = logits;
@@ -208,10 +243,8 @@ extern "C" int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, 
   p.accept_len = accept_len;
   p.next_x0 = next_x0;
   p.packed = packed;
-  const size_t parts = static_cast<size_t>(bs) * W * p.n_chunks;
   p.counters = static_cast<uint32_t*>(workspace);
-  p.part_v = reinterpret_cast<float*>(static_cast<char*>(workspace) + COUNTER_BYTES);
-  p.part_i = reinterpret_cast<int32_t*>(p.part_v + parts);
+  p.part = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + PARTS_OFFSET);
   const dim3 grid(p.n_chunks, bs * W);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GSS_BF16)
@@ -243,10 +276,8 @@ struct UnmaskParams {
   int32_t* n_unmasked;  // [bs] or null
   int32_t* n_left;      // [bs] or null
   int32_t* seed_out;    // [bs] or null
-  float* part_m;        // [bs*W, n_chunks]
-  int32_t* part_i;
-  float* part_s;
-  uint32_t* counters;   // [bs]
+  u32x4_t* part;        // [bs*W, n_chunks] (max bits, index, sum bits, 0)
+  uint32_t* counters;   // arrival counters (see arrive_last)
 };
 
 // merge (om, oi, os) into (m, i, s): the greedy winner, and the exp-sums rescaled to its value. A part whose max is
@@ -295,76 +326,96 @@ __global__ void __launch_bounds__(ARG_THREADS) unmask_step_kernel(UnmaskParams p
   if (tid == 0) {
     for (int w = 1; w < ARG_THREADS / 64; ++w) merge_softmax(m, mi, s, wm[w], wi[w], ws[w]);
     const int64_t slot = static_cast<int64_t>(row) * p.n_chunks + chunk;
-    st_agent(reinterpret_cast<uint32_t*>(p.part_m + slot), __float_as_uint(m));
-    st_agent(reinterpret_cast<uint32_t*>(p.part_i + slot), static_cast<uint32_t>(mi));
-    st_agent(reinterpret_cast<uint32_t*>(p.part_s + slot), __float_as_uint(s));
+    st_agent_x4(p.part + slot, u32x4_t{__float_as_uint(m), static_cast<uint32_t>(mi), __float_as_uint(s), 0u});
     wait_stores();
-    is_last = count_arrival(&p.counters[b]) == static_cast<uint32_t>(p.n_chunks * p.W - 1);
+    const int r = row - b * p.W;
+    is_last = arrive_last(p.counters, b, r * p.n_chunks + chunk, p.W * p.n_chunks);
   }
   __syncthreads();
   if (!is_last) return;
 
   // ---- phase 2: this workgroup finishes sequence b ------------------------------------------------------------
+  // the chunk results of its W rows, one (row, chunk) per thread (coherent loads), then each row in chunk order
+  __shared__ float cm_s[MAX_W * MAX_CHUNKS], cs_s[MAX_W * MAX_CHUNKS];
+  __shared__ int ci_s[MAX_W * MAX_CHUNKS];
   __shared__ int rx[MAX_W];
   __shared__ float rc[MAX_W];
+  __shared__ int blk_s[MAX_W];
+  int32_t* blk = p.block + static_cast<int64_t>(b) * p.W;
+  if (tid < p.W) blk_s[tid] = blk[tid];
+  {
+    const u32x4_t* base = p.part + static_cast<int64_t>(b) * p.W * p.n_chunks;
+    const int n_items = p.W * p.n_chunks;
+    for (int t0 = tid; t0 < n_items; t0 += 2 * ARG_THREADS) {  // two items per thread and memory round trip
+      const int t1 = t0 + ARG_THREADS < n_items ? t0 + ARG_THREADS : t0;
+      u32x4_t q0, q1, u2, u3;
+      ld_agent_x4(2, base + t0, base + t1, nullptr, nullptr, q0, q1, u2, u3);
+      cm_s[t0] = __uint_as_float(q0[0]);
+      ci_s[t0] = static_cast<int>(q0[1]);
+      cs_s[t0] = __uint_as_float(q0[2]);
+      cm_s[t1] = __uint_as_float(q1[0]);
+      ci_s[t1] = static_cast<int>(q1[1]);
+      cs_s[t1] = __uint_as_float(q1[2]);
+    }
+  }
+  __syncthreads();
   if (tid < p.W) {
-    const int64_t base = (static_cast<int64_t>(b) * p.W + tid) * p.n_chunks;
-    const uint32_t* pm = reinterpret_cast<const uint32_t*>(p.part_m) + base;
-    const uint32_t* pi = reinterpret_cast<const uint32_t*>(p.part_i) + base;
-    const uint32_t* ps = reinterpret_cast<const uint32_t*>(p.part_s) + base;
-    float M = __uint_as_float(ld_agent(pm)), S = __uint_as_float(ld_agent(ps));
-    int I = static_cast<int>(ld_agent(pi));
-    for (int c = 1; c < p.n_chunks; ++c)
-      merge_softmax(M, I, S, __uint_as_float(ld_agent(pm + c)), static_cast<int>(ld_agent(pi + c)),
-                    __uint_as_float(ld_agent(ps + c)));
+    const int r0 = tid * p.n_chunks;
+    float M = cm_s[r0], S = cs_s[r0];
+    int I = ci_s[r0];
+    for (int c = 1; c < p.n_chunks; ++c) merge_softmax(M, I, S, cm_s[r0 + c], ci_s[r0 + c], cs_s[r0 + c]);
     // a NaN or +inf in the row, or a row of -inf, makes the whole fp32 softmax NaN: argmax 0, probability NaN
     const bool finite_max = M == M && M != INFINITY && M != -INFINITY;
     rx[tid] = finite_max ? I : 0;
     rc[tid] = finite_max ? 1.f / S : __builtin_nanf("");
   }
   __syncthreads();
-  int32_t* blk = p.block + static_cast<int64_t>(b) * p.W;
   if (tid < p.W) {
     const int src = tid > 0 ? tid - 1 : 0;
     if (p.x1_out) p.x1_out[static_cast<int64_t>(b) * p.W + tid] = rx[src];
     if (p.conf_out) p.conf_out[static_cast<int64_t>(b) * p.W + tid] = rc[src];
   }
-  if (tid == 0) {
-    // the forced position: first argmax of conf over masked positions (-inf elsewhere; NaN as max)
-    float best = -INFINITY;
-    int bj = 0x7fffffff;
-    for (int j = 0; j < p.W; ++j) {
-      const float c = blk[j] == p.mask_id ? rc[j > 0 ? j - 1 : 0] : -INFINITY;
-      if (beats(c, j, best, bj)) { best = c; bj = j; }
+  if (tid < 64) {
+    // the unmask rule with one lane per position of wave 0: the forced position is the first argmax of conf over
+    // the masked positions (-inf elsewhere; NaN as max), found by an xor-shuffle reduction under the same total
+    // order; counts by ballot
+    const int j = tid;
+    const int src = j > 0 ? j - 1 : 0;
+    const bool masked = j < p.W && blk_s[j] == p.mask_id;
+    const float c = masked ? rc[src] : -INFINITY;
+    float best = c;
+    int bj = j < p.W ? j : 0x7fffffff;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ob = __shfl_xor(best, o, 64);
+      const int oj = __shfl_xor(bj, o, 64);
+      if (beats(ob, oj, best, bj)) { best = ob; bj = oj; }
     }
-    int un = 0, left = 0;
-    for (int j = 0; j < p.W; ++j) {
-      if (blk[j] != p.mask_id) continue;
-      const int src = j > 0 ? j - 1 : 0;
-      if (rc[src] > p.threshold || j == bj) {
-        blk[j] = rx[src];
-        ++un;
-      }
-      left += blk[j] == p.mask_id;  // a position unmasked to the mask id itself stays masked, as in the reference
+    const bool un = masked && (c > p.threshold || j == bj);
+    const int nv = un ? rx[src] : (j < p.W ? blk_s[j] : 0);
+    if (un) blk[j] = nv;
+    // a position unmasked to the mask id itself stays masked, as in the reference
+    const uint64_t left = __ballot(j < p.W && nv == p.mask_id), unm = __ballot(un);
+    if (j == 0) {
+      if (p.n_unmasked) p.n_unmasked[b] = __popcll(unm);
+      if (p.n_left) p.n_left[b] = __popcll(left);
+      if (p.seed_out) p.seed_out[b] = rx[p.W - 1];
+      reset_counter(seq_counter(p.counters, b));
     }
-    if (p.n_unmasked) p.n_unmasked[b] = un;
-    if (p.n_left) p.n_left[b] = left;
-    if (p.seed_out) p.seed_out[b] = rx[p.W - 1];
-    reset_counter(&p.counters[b]);
   }
 }
 
 size_t unmask_ws_bytes(int bs, int W, int V) {
   const size_t nc = (static_cast<size_t>(V) + CHUNK - 1) / CHUNK;
   const size_t parts = static_cast<size_t>(bs) * W * nc;
-  return COUNTER_BYTES + parts * (2 * sizeof(float) + sizeof(int32_t));
+  return PARTS_OFFSET + parts * sizeof(u32x4_t);
 }
 
 }  // namespace
 
 extern "C" int gss_unmask_workspace_size(int bs, int W, int V, size_t* bytes) {
   if (!bytes || bs <= 0 || W <= 0 || V <= 0) return GSS_ERR_ARG;
-  if (W > MAX_W) return GSS_ERR_UNSUPPORTED;
+  if (W > MAX_W || V > MAX_CHUNKS * CHUNK) return GSS_ERR_UNSUPPORTED;
   *bytes = unmask_ws_bytes(bs, W, V);
   return GSS_OK;
 }
@@ -375,7 +426,7 @@ extern "C" int gss_unmask_step(const void* logits, int dtype, int64_t ld_row, in
                                gss_stream_t stream) {
   if (!logits || !block || bs <= 0 || W <= 0 || V <= 0 || ld_row < V) return GSS_ERR_ARG;
   if (dtype != GSS_BF16 && dtype != GSS_F32) return GSS_ERR_ARG;
-  if (W > MAX_W || bs > static_cast<int>(COUNTER_BYTES / sizeof(uint32_t))) return GSS_ERR_UNSUPPORTED;
+  if (W > MAX_W || V > MAX_CHUNKS * CHUNK || bs > MAX_SEQ) return GSS_ERR_UNSUPPORTED;
   if (!workspace || workspace_bytes < unmask_ws_bytes(bs, W, V)) return GSS_ERR_WORKSPACE;
   UnmaskParams p;
   p.logits = logits;
@@ -391,11 +442,8 @@ extern "C" int gss_unmask_step(const void* logits, int dtype, int64_t ld_row, in
   p.n_unmasked = n_unmasked;
   p.n_left = n_left;
   p.seed_out = seed;
-  const size_t parts = static_cast<size_t>(bs) * W * p.n_chunks;
   p.counters = static_cast<uint32_t*>(workspace);
-  p.part_m = reinterpret_cast<float*>(static_cast<char*>(workspace) + COUNTER_BYTES);
-  p.part_s = p.part_m + parts;
-  p.part_i = reinterpret_cast<int32_t*>(p.part_s + parts);
+  p.part = reinterpret_cast<u32x4_t*>(static_cast<char*>(workspace) + PARTS_OFFSET);
   const dim3 grid(p.n_chunks, bs * W);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == GSS_BF16)

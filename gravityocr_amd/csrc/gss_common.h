@@ -68,4 +68,68 @@ GSS_DEV uint32_t count_arrival(uint32_t* ctr) {
 }
 GSS_DEV void reset_counter(uint32_t* ctr) { __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
+// Coherent 16-byte store (st_agent's sc1 form of global_store_dwordx4); 16-byte aligned.
+GSS_DEV void st_agent_x4(void* p, u32x4_t v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+
+// Batched coherent 4-byte loads (ld_agent's instruction), n (1..3) issued back to back and waited for once.
+GSS_DEV void ld_agent_u32(int n, const uint32_t* p0, const uint32_t* p1, const uint32_t* p2, uint32_t& r0,
+                          uint32_t& r1, uint32_t& r2) {
+  switch (n) {
+    case 1:
+      asm volatile("global_load_dword %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=&v"(r0) : "v"(p0) : "memory");
+      break;
+    case 2:
+      asm volatile("global_load_dword %0, %2, off sc1\n\tglobal_load_dword %1, %3, off sc1\n\ts_waitcnt vmcnt(0)"
+                   : "=&v"(r0), "=&v"(r1)
+                   : "v"(p0), "v"(p1)
+                   : "memory");
+      break;
+    default:
+      asm volatile(
+          "global_load_dword %0, %3, off sc1\n\tglobal_load_dword %1, %4, off sc1\n\t"
+          "global_load_dword %2, %5, off sc1\n\ts_waitcnt vmcnt(0)"
+          : "=&v"(r0), "=&v"(r1), "=&v"(r2)
+          : "v"(p0), "v"(p1), "v"(p2)
+          : "memory");
+      break;
+  }
+}
+
+// Batched coherent 16-byte loads for handed-over data: ld_agent's sc1 form of global_load_dwordx4, n (1..4) of them
+// issued back to back and waited for once inside the same asm statement (the compiler waits after every atomic load,
+// which serializes a series of ld_agent calls into one memory round trip each). Pointers must be 16-byte aligned.
+GSS_DEV void ld_agent_x4(int n, const void* p0, const void* p1, const void* p2, const void* p3, u32x4_t& r0,
+                         u32x4_t& r1, u32x4_t& r2, u32x4_t& r3) {
+  switch (n) {
+    case 1:
+      asm volatile("global_load_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)" : "=&v"(r0) : "v"(p0) : "memory");
+      break;
+    case 2:
+      asm volatile(
+          "global_load_dwordx4 %0, %2, off sc1\n\tglobal_load_dwordx4 %1, %3, off sc1\n\ts_waitcnt vmcnt(0)"
+          : "=&v"(r0), "=&v"(r1)
+          : "v"(p0), "v"(p1)
+          : "memory");
+      break;
+    case 3:
+      asm volatile(
+          "global_load_dwordx4 %0, %3, off sc1\n\tglobal_load_dwordx4 %1, %4, off sc1\n\t"
+          "global_load_dwordx4 %2, %5, off sc1\n\ts_waitcnt vmcnt(0)"
+          : "=&v"(r0), "=&v"(r1), "=&v"(r2)
+          : "v"(p0), "v"(p1), "v"(p2)
+          : "memory");
+      break;
+    default:
+      asm volatile(
+          "global_load_dwordx4 %0, %4, off sc1\n\tglobal_load_dwordx4 %1, %5, off sc1\n\t"
+          "global_load_dwordx4 %2, %6, off sc1\n\tglobal_load_dwordx4 %3, %7, off sc1\n\ts_waitcnt vmcnt(0)"
+          : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+          : "v"(p0), "v"(p1), "v"(p2), "v"(p3)
+          : "memory");
+      break;
+  }
+}
+
 inline int gss_launch_status() { return hipGetLastError() == hipSuccess ? GSS_OK : GSS_ERR_LAUNCH; }

@@ -128,28 +128,35 @@ GSS_DEV void addnorm_row(const GemmParams& p, int row, int lane, uint16_t* xs, b
   }
 }
 
-// Post-norm of one row (one wavefront; H = p.N = 64 * E, E <= 32): the arithmetic, order and rounding points of
-// gss_add_rmsnorm, so the fused and separate norms agree bit for bit.
+// Post-norm of one row (one wavefront; H = p.N = 64 * E with E = 8 * nc, nc <= 4): the arithmetic, order and
+// rounding points of gss_add_rmsnorm, so the fused and separate norms agree bit for bit. The GEMM output rows were
+// handed over through the coherence point (coherent loads); h and the weights were written before this kernel.
 constexpr int POST_MAX_E = 32;
 GSS_DEV void post_addnorm_row(const GemmParams& p, int row, int lane) {
-  const int E = p.N / 64;
+  const int E = p.N / 64, nc = E / 8;
   const int64_t off = static_cast<int64_t>(row) * p.N + lane * E;
-  const uint32_t* a = reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.y) + off);  // E is even
+  const uint16_t* a = static_cast<const uint16_t*>(p.y) + off;
+  u32x4_t qa[4];
+  ld_agent_x4(nc, a, a + 8 * min(1, nc - 1), a + 8 * min(2, nc - 1), a + 8 * min(3, nc - 1), qa[0], qa[1], qa[2],
+              qa[3]);
   float av[POST_MAX_E], hv[POST_MAX_E], wp[POST_MAX_E], wn[POST_MAX_E];
 #pragma unroll
-  for (int e = 0; e < POST_MAX_E; e += 2) {
-    if (e < E) {
-      const uint32_t u = ld_agent(a + e / 2);  // written by the other workgroups of this launch
-      av[e] = __uint_as_float(u << 16);
-      av[e + 1] = __uint_as_float(u & 0xffff0000u);
-    }
-  }
+  for (int c = 0; c < POST_MAX_E / 8; ++c) {
+    if (c < nc) {
+      const u32x4_t qh = *reinterpret_cast<const u32x4_t*>(p.post_h + off + 8 * c);
+      const u32x4_t qp = *reinterpret_cast<const u32x4_t*>(p.post_wp + lane * E + 8 * c);
+      const u32x4_t qn = *reinterpret_cast<const u32x4_t*>(p.post_wn + lane * E + 8 * c);
 #pragma unroll
-  for (int e = 0; e < POST_MAX_E; ++e) {
-    if (e < E) {
-      hv[e] = bf16_to_f32(p.post_h[off + e]);
-      wp[e] = bf16_to_f32(p.post_wp[lane * E + e]);
-      wn[e] = bf16_to_f32(p.post_wn[lane * E + e]);
+      for (int e = 0; e < 4; ++e) {
+        av[8 * c + 2 * e] = __uint_as_float(qa[c][e] << 16);
+        av[8 * c + 2 * e + 1] = __uint_as_float(qa[c][e] & 0xffff0000u);
+        hv[8 * c + 2 * e] = __uint_as_float(qh[e] << 16);
+        hv[8 * c + 2 * e + 1] = __uint_as_float(qh[e] & 0xffff0000u);
+        wp[8 * c + 2 * e] = __uint_as_float(qp[e] << 16);
+        wp[8 * c + 2 * e + 1] = __uint_as_float(qp[e] & 0xffff0000u);
+        wn[8 * c + 2 * e] = __uint_as_float(qn[e] << 16);
+        wn[8 * c + 2 * e + 1] = __uint_as_float(qn[e] & 0xffff0000u);
+      }
     }
   }
   float ss = 0.f;
@@ -167,10 +174,18 @@ GSS_DEV void post_addnorm_row(const GemmParams& p, int row, int lane) {
   }
   const float rh = 1.f / sqrtf(wave_sum(sh) / static_cast<float>(p.N) + p.post_eps);
 #pragma unroll
-  for (int e = 0; e < POST_MAX_E; ++e) {
-    if (e < E) {
-      p.post_h[off + e] = f32_to_bf16(hv[e]);
-      p.post_x[off + e] = f32_to_bf16(wn[e] * round_bf16(hv[e] * rh));
+  for (int c = 0; c < POST_MAX_E / 8; ++c) {
+    if (c < nc) {
+      const float* h8 = hv + 8 * c;
+      float x8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x8[e] = wn[8 * c + e] * round_bf16(h8[e] * rh);
+      *reinterpret_cast<u32x4_t*>(p.post_h + off + 8 * c) =
+          u32x4_t{pack_bf16x2(h8[0], h8[1]), pack_bf16x2(h8[2], h8[3]), pack_bf16x2(h8[4], h8[5]),
+                  pack_bf16x2(h8[6], h8[7])};
+      *reinterpret_cast<u32x4_t*>(p.post_x + off + 8 * c) =
+          u32x4_t{pack_bf16x2(x8[0], x8[1]), pack_bf16x2(x8[2], x8[3]), pack_bf16x2(x8[4], x8[5]),
+                  pack_bf16x2(x8[6], x8[7])};
     }
   }
 }
@@ -359,12 +374,16 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
       for (int n = 0; n < NT; ++n) {
         if ((f * NT + n) % NW != wv || !live(f, n)) continue;
         floatx4_t s = {0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < p.ksplit; ++k) {  // split order
-          const uint64_t* src = part_at(k, f, n);
-          const uint64_t lo = ld_agent(src), hi = ld_agent(src + 1);
-          const floatx4_t v = {__uint_as_float(static_cast<uint32_t>(lo)), __uint_as_float(static_cast<uint32_t>(lo >> 32)),
-                               __uint_as_float(static_cast<uint32_t>(hi)), __uint_as_float(static_cast<uint32_t>(hi >> 32))};
-          s = k == 0 ? v : s + v;
+        for (int k0 = 0; k0 < p.ksplit; k0 += 4) {  // up to 4 partials per memory round trip, summed in split order
+          const int nk = min(4, p.ksplit - k0);
+          u32x4_t v[4];
+          ld_agent_x4(nk, part_at(k0, f, n), part_at(min(k0 + 1, p.ksplit - 1), f, n),
+                      part_at(min(k0 + 2, p.ksplit - 1), f, n), part_at(min(k0 + 3, p.ksplit - 1), f, n), v[0], v[1],
+                      v[2], v[3]);
+          for (int j = 0; j < nk; ++j) {
+            const floatx4_t x = __builtin_bit_cast(floatx4_t, v[j]);
+            s = k0 + j == 0 ? x : s + x;
+          }
         }
         epilogue(f, n, s);
       }
@@ -486,7 +505,11 @@ int gemm_entry(GemmParams& p, int epi, void* ws, size_t ws_bytes, hipStream_t st
   if (post) {
     if (pro || epi != EPI_PLAIN || p.out_f32 || p.ldy != p.N) return GSS_ERR_ARG;
     if (!p.post_wp || !p.post_wn || !p.post_x || p.post_x == p.post_h) return GSS_ERR_ARG;
-    if (p.N % 128 != 0 || p.N / 64 > POST_MAX_E) return GSS_ERR_UNSUPPORTED;  // an even count per lane
+    if (p.N % 512 != 0 || p.N / 64 > POST_MAX_E) return GSS_ERR_UNSUPPORTED;  // 8-element chunks per lane
+    if ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.post_h) |
+         reinterpret_cast<uintptr_t>(p.post_x) | reinterpret_cast<uintptr_t>(p.post_wp) |
+         reinterpret_cast<uintptr_t>(p.post_wn)) & 15u)
+      return GSS_ERR_ARG;
     return launch_epi<EPI_PLAIN, PRO_NONE, true>(p, ws, ws_bytes, st);
   }
   if (pro) {

@@ -99,8 +99,9 @@ int gss_verify_attn(const void* q, const void* k_pages, const void* v_pages, con
  *   next_x0[b]    = target[b, accept_len[b]]              (the correction, or the bonus when all W-1 matched)
  *   packed[b]     = (window[b,0], accept_len[b], target[b,0..W-1] with entries past accept_len zeroed)
  *                   the row layout of _ss_commit_kernel's readback (selfspec_fast_commit.py:125-138); may be NULL.
- * Workspace: gss_argmax_workspace_size bytes, zeroed once after allocation. Its first 4 KiB are per-sequence
- * counters at a fixed offset, so one workspace serves calls with different W (sized for the largest).
+ * Workspace: gss_argmax_workspace_size bytes, zeroed once after allocation. Its first 1152 KiB are arrival counters
+ * (nine 128-byte lines per sequence) at a fixed offset, so one workspace serves calls with different bs, W, V (sized
+ * for the largest). bs <= 1024, W <= 64, V <= 131072.
  */
 int gss_argmax_workspace_size(int bs, int W, int V, size_t* bytes);
 
@@ -120,8 +121,8 @@ int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, int bs, int
  * unmasked), n_left[b] (positions holding mask_id afterwards), seed[b] = argmax of row W - 1 without shift (the next block's seed after the commit forward,
  * src/fast_sampling.py:187-190). A block without masks is left unchanged. conf is 1 / sum(exp(x - max)), summed in
  * a fixed order (within a few ulp of torch's softmax).
- * Workspace: gss_unmask_workspace_size bytes, zeroed once after allocation (the first 4 KiB are per-sequence
- * counters, the same layout as the argmax workspace).
+ * Workspace: gss_unmask_workspace_size bytes, zeroed once after allocation (the first 1152 KiB are counters, the
+ * same layout and limits as the argmax workspace).
  */
 int gss_unmask_workspace_size(int bs, int W, int V, size_t* bytes);
 
@@ -179,7 +180,8 @@ int gss_gemm_set_policy(int max_waves, int features_per_wg, int max_ksplit);
 /* Norm epilogue of gss_gemm (the sandwich norm after o_proj and after the MLP down projection,
  * modeling_glm_ocr.py:263-310): once Y = X W^T is written (bf16, ldy == N, N = hidden size), every row gets
  *   h = h + rmsnorm(Y) * w_post;   x = rmsnorm(h) * w_next
- * with the arithmetic of gss_add_rmsnorm (bit-identical results). h is updated in place. */
+ * with the arithmetic of gss_add_rmsnorm (bit-identical results). h is updated in place. Needs N % 512 == 0,
+ * N <= 2048 and 16-byte aligned y, h, x and weights. The last workgroup to finish runs the norm. */
 typedef struct gss_norm_epilogue {
   const void* w_post;
   void* h;

@@ -35,18 +35,21 @@ def test_host_side_queries_and_status_strings():
     assert L.gss_status_string(OK) == b"ok"
     assert L.gss_status_string(WORKSPACE).startswith(b"workspace")
     n = ctypes.c_size_t(0)
-    # argmax: counters (4 KiB) + chunk winners (value + index) of ceil(V / 4096) chunks per row
+    # argmax: arrival counters (1024 sequences x 9 lines of 128 B) + chunk winners (value, index) of ceil(V / 4096)
+    # chunks per row
+    ctr = 1024 * 9 * 128
     assert L.gss_argmax_workspace_size(2, 17, 59392, ctypes.byref(n)) == OK
-    assert n.value == 4096 + 2 * 17 * 15 * 8
+    assert n.value == ctr + 2 * 17 * 15 * 8
+    assert L.gss_argmax_workspace_size(1, 17, 131073, ctypes.byref(n)) == UNSUPPORTED
     assert L.gss_argmax_workspace_size(1, 65, 100, ctypes.byref(n)) == UNSUPPORTED
     assert L.gss_argmax_workspace_size(0, 17, 100, ctypes.byref(n)) == ARG
     assert L.gss_attn_workspace_size(1, 16, 2, 128, 17, 8192, ctypes.byref(n)) == OK and n.value > 0
     assert L.gss_attn_workspace_size(1, 16, 3, 128, 17, 8192, ctypes.byref(n)) == UNSUPPORTED   # Hq % Hkv
     assert L.gss_attn_workspace_size(1, 16, 2, 96, 17, 8192, ctypes.byref(n)) == UNSUPPORTED    # head dim
     assert L.gss_kv_commit_workspace_size(4, ctypes.byref(n)) == OK
-    # unmask: counters (4 KiB) + chunk (max, sum, index) of ceil(V / 4096) chunks per row
+    # unmask: the same counters + chunk (max, index, sum) of ceil(V / 4096) chunks per row, 16 B each
     assert L.gss_unmask_workspace_size(2, 32, 59392, ctypes.byref(n)) == OK
-    assert n.value == 4096 + 2 * 32 * 15 * 12
+    assert n.value == ctr + 2 * 32 * 15 * 16
     assert L.gss_unmask_workspace_size(1, 65, 100, ctypes.byref(n)) == UNSUPPORTED
 
 

@@ -130,7 +130,7 @@ def test_unmask_kernel_reuses_its_workspace(cuda):
     different shapes, gives the same results as a fresh one."""
     from gravityocr_amd.kernels import unmask_workspace_bytes
     ws = torch.full((unmask_workspace_bytes(3, 32, 59392),), 0xFF, dtype=torch.uint8, device=cuda)
-    ws[:4096] = 0
+    ws[:1024 * 9 * 128] = 0                                # the counter block
     g = torch.Generator().manual_seed(5)
     for bs, W, V in [(3, 32, 59392), (1, 4, 100), (2, 17, 9000), (3, 32, 59392)]:
         logits = torch.randn(bs, W, V, generator=g).bfloat16()

@@ -161,10 +161,10 @@ def test_gemm_split_k_parity_and_invariance(cuda, ksplit_policy, M, N, Kd):
 
 
 @pytest.mark.parametrize("M", [1, 17, 64])
-@pytest.mark.parametrize("N,Kd", [(1536, 2048), (1536, 4608), (256, 704)])
+@pytest.mark.parametrize("N,Kd", [(1536, 2048), (1536, 4608), (512, 704), (2048, 1536)])
 def test_post_norm_epilogue_equals_separate_norm(cuda, ksplit_policy, M, N, Kd):
     """gss_norm_epilogue (h += rmsnorm(Y) * w_post; x = rmsnorm(h) * w_next inside the GEMM) == the plain GEMM followed
-    by gss_add_rmsnorm, bit for bit, for split-K (N = 1536) and unsplit shapes."""
+    by gss_add_rmsnorm, bit for bit, for split-K (Kd = 4608) and unsplit shapes, 1 to 4 chunks of 8 per lane."""
     from gravityocr_amd.kernels import add_rmsnorm, gemm
     g = torch.Generator().manual_seed(M * 3 + N + Kd)
     x = torch.randn(M, Kd, generator=g).bfloat16().to(cuda)
@@ -182,6 +182,18 @@ def test_post_norm_epilogue_equals_separate_norm(cuda, ksplit_policy, M, N, Kd):
         gemm(x, w, a, workspace=ws, post=dict(h=h2, w_post=wp, w_next=wn, x=x2, eps=1e-5))
         torch.cuda.synchronize()
         assert torch.equal(a, a_ref) and torch.equal(h2, h_ref) and torch.equal(x2, x_ref), rep
+
+
+def test_post_norm_epilogue_rejects_other_widths(cuda):
+    from gravityocr_amd._lib import GssError
+    from gravityocr_amd.kernels import gemm
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=cuda)
+    w = torch.zeros(256, 256, dtype=torch.bfloat16, device=cuda)
+    y, h, xo = (torch.zeros(4, 256, dtype=torch.bfloat16, device=cuda) for _ in range(3))
+    one = torch.ones(256, dtype=torch.bfloat16, device=cuda)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=cuda)
+    with pytest.raises(GssError, match="unsupported"):
+        gemm(x, w, y, workspace=ws, post=dict(h=h, w_post=one, w_next=one, x=xo, eps=1e-5))
 
 
 def test_split_k_shapes_share_one_workspace(cuda, ksplit_policy):
