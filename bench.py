@@ -67,6 +67,35 @@ def attn_roofline(dev, L, W, cap, n_causal=1, copies=ATTN_COPIES, Hq=16, Hkv=2, 
     return time_kernel(fns, n=2)
 
 
+def attn_batched_roofline(dev, W=17, bs=32, copies=2, Hq=16, Hkv=2, D=128, seed=3):
+    """The batched draft attention (bs sequences, prefixes L_i ~ U[1024, 12288] with a seeded generator, one shared
+    pool of 16-token pages in shuffled order, window W): average call duration over ``copies`` distinct pools (each
+    ~0.4 GB, together more than the Infinity Cache). Returns (microseconds per call, algorithmic bytes per call)."""
+    from gravityocr_amd import kernels as K
+    Ls = np.random.default_rng(seed).integers(1024, 12289, size=bs)
+    cap = int(Ls.max()) + W + 64
+    ppseq = (cap + 15) // 16
+    g = torch.Generator(device=dev).manual_seed(seed)
+    n_pages = bs * ppseq
+    pools = []
+    for _ in range(copies):
+        kp = torch.empty(n_pages, Hkv, 16, D, dtype=torch.bfloat16, device=dev).normal_(0, D ** -0.5, generator=g)
+        vp = torch.empty(n_pages, Hkv, D, 16, dtype=torch.bfloat16, device=dev).normal_(0, D ** -0.5, generator=g)
+        pools.append((kp, vp))
+    pt = torch.randperm(n_pages, device=dev, generator=g).int().view(bs, ppseq)
+    q = torch.randn(bs, W, Hq, D, device=dev, generator=g).div_(D ** 0.5).bfloat16()
+    kw = torch.randn(bs, W, Hkv, D, device=dev, generator=g).div_(D ** 0.5).bfloat16()
+    vw = torch.randn_like(kw)
+    o = torch.empty_like(q)
+    sl = torch.tensor(Ls, dtype=torch.int32, device=dev)
+    ws = torch.zeros(max(1, K.attn_workspace_bytes(bs, Hq, Hkv, D, W, cap)), dtype=torch.uint8, device=dev)
+    fns = [lambda kp=kp, vp=vp: K.window_attention(q, kp, vp, pt, sl, kw, vw, o, n_causal=1, scale=D ** -0.5,
+                                                   max_kv_len=cap, workspace=ws) for kp, vp in pools]
+    us = time_kernel(fns, n=4, reps=3)
+    nbytes = sum(2 * Hkv * D * 2 * (int(L) + W) for L in Ls) + 2 * bs * W * Hq * D * 2
+    return us, nbytes
+
+
 def copy_calibration(dev, reps=3):
     """Plain device copies of COPY_BYTES, as an elementwise kernel (reads COPY_BYTES, writes COPY_BYTES): the
     calibration kernel of the FETCH_SIZE / WRITE_SIZE passes."""
@@ -128,6 +157,8 @@ def main():
     ap.add_argument("--profile-only", action="store_true", help="skip AR, planted and CPU legs (for rocprof runs)")
     ap.add_argument("--attn-only", action="store_true",
                     help="only the draft-attention roofline measurement and the copy calibration (for rocprof runs)")
+    ap.add_argument("--attn-batched-only", action="store_true",
+                    help="only the batched (32 ragged sequences) draft-attention measurement (for rocprof runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the self-spec round shards by sequence (no collective), so a multi-GPU "
@@ -144,6 +175,12 @@ def main():
         print(json.dumps({"kernel": "gss_draft_attn", "L": L, "W": Kw, "avg_us": round(d_us, 2),
                           "algorithmic_bytes": ab, "achieved_GBs": round(ab / (d_us * 1e-6) / 1e9, 1),
                           "copy_bytes": COPY_BYTES}), flush=True)
+        return
+    if args.attn_batched_only:
+        b_us, b_bytes = attn_batched_roofline(torch.device("cuda:0"), W=args.bd + 1)
+        print(json.dumps({"kernel": "gss_draft_attn batched", "W": args.bd + 1, "avg_us": round(b_us, 2),
+                          "algorithmic_bytes": b_bytes, "achieved_GBs": round(b_bytes / (b_us * 1e-6) / 1e9, 1)}),
+              flush=True)
         return
 
     from gravityocr_amd.engine import GssEngine, SelfSpecDecoder
@@ -291,6 +328,8 @@ def main():
     achieved = ab / (d_us * 1e-6) / 1e9
     tflops = attn_flops(L, Kw) / (d_us * 1e-6) / 1e12
     log(f"draft attention L={L}: {d_us:.2f} us, {achieved:.0f} GB/s, {tflops:.1f} TFLOP/s; verify {v_us:.2f} us")
+    b_us, b_bytes = attn_batched_roofline(dev)
+    log(f"batched draft attention (32 ragged sequences): {b_us:.2f} us, {b_bytes / (b_us * 1e-6) / 1e9:.0f} GB/s")
 
     # ---- CPU baseline: the oracle's round on the host cores, from the same 8K state -----------------------------
     cpu = None
@@ -350,6 +389,11 @@ def main():
                      "algorithmic_bytes": ab, "avg_us": round(d_us, 2), "L": L, "W": Kw,
                      "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "verify_avg_us": round(v_us, 2)},
+        "roofline_batched": {"bound": "hbm", "kernel": "gss_draft_attn, 32 sequences, prefixes U[1024, 12288] "
+                                                       "(seed 3), W=17, one paged pool",
+                             "achieved": round(b_bytes / (b_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(b_bytes / (b_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                             "algorithmic_bytes": b_bytes, "avg_us": round(b_us, 2)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -65,15 +65,16 @@ const char* gss_status_string(int status);
  *                             n_causal = 0 is natcache round 0 and the block-diffusion sampler's full block.
  *   verify (gss_verify_attn): row w sees window rows 0..w (causal, bottom-right aligned).
  * scale multiplies q.k (1/sqrt(D) for GLM). max_kv_len is the cache capacity: every L must be <= max_kv_len. It
- * alone (with the split policy) fixes how the keys are partitioned, so calls with different W or L on the same
- * cache combine every key in the same order (a verify row equals the AR step of the same token bit for bit). The
+ * and bs * Hkv (with the split policy) fix how the keys are partitioned, so calls with different W or L on the same
+ * cache and batch size combine every key in the same order (a verify row equals the AR step of the same token bit
+ * for bit; rows of different batch sizes agree bit for bit whenever their plans coincide). The
  * workspace holds gss_attn_workspace_size(...) bytes (no zeroing needed). Supported: D in {64, 128}, page = 16,
  * 1 <= W <= 64, Hq % Hkv == 0, max_kv_len + 64 <= 256 * 256 * 64 keys.
  */
 int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes);
 
 /* Split-KV policy of both attention kernels: about target_wgs / (bs * Hkv) key splits per sequence and kv head, each
- * covering at least min_tiles 64-token tiles (defaults 256 and 4; min_tiles <= 256). Process-wide; set it before
+ * covering at least min_tiles 64-token tiles (defaults 512 and 4; min_tiles <= 256). Process-wide; set it before
  * sizing workspaces, and keep it fixed while a cache is decoded (it is part of the key partition). */
 int gss_attn_set_split_policy(int target_wgs, int min_tiles);
 

@@ -113,7 +113,7 @@ def test_split_policies(cuda, policy):
         run_case(cuda, [5000], 17, 1, seed=21)
         run_case(cuda, [5000, 17, 700], 17, 1, seed=22, verify=True, max_kv_len=6000)
     finally:
-        assert lib().gss_attn_set_split_policy(256, 4) == 0
+        assert lib().gss_attn_set_split_policy(512, 4) == 0
 
 
 def test_stale_workspace(cuda):
