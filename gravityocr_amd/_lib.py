@@ -17,6 +17,7 @@ SIGNATURES = {
     "gss_status_string": ([_i], ctypes.c_char_p),
     "gss_attn_workspace_size": ([_i, _i, _i, _i, _i, _i, _psz], _i),
     "gss_attn_set_split_policy": ([_i, _i], _i),
+    "gss_attn_set_wide_min": ([_i], _i),
     "gss_draft_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
     "gss_verify_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
     "gss_argmax_workspace_size": ([_i, _i, _i, _psz], _i),

@@ -4,10 +4,13 @@
 //
 // gfx950 design
 //   * GQA packing: the G = Hq/Hkv query heads of one KV head and the W window rows form R = G*W query rows that
-//     share every K/V byte read (row n = w*G + g); rows are MFMA N-tiles of 16. A workgroup owns a row group of up
-//     to NTG = 3 N-tiles, so the MFMA work of one key tile is spread over ceil(R/48) workgroups. Those row groups
-//     of a split are launched on the same XCD (grid x = row_group * S8 + split with S8 a multiple of 8, and
-//     workgroups are dealt to the 8 XCDs round-robin), so their repeated K/V reads hit that XCD's L2.
+//     share every K/V byte read (row n = w*G + g); rows are MFMA N-tiles of 16. One workgroup takes a unit
+//     (sequence, kv head, key split) for all its rows (up to 10 N-tiles; wider windows use several row groups), so
+//     each K/V byte of the split enters the CU's LDS once.
+//   * Waves are (row wave, key lane) pairs, at most 4, one per SIMD: a row wave owns NGW <= 5 N-tiles (Q fragments
+//     in registers, the O and S accumulators in AGPRs), key lane kl
+//     takes the split's tiles j with j % 2 == kl, whole (64 keys). Each wave runs its own online softmax, so no data
+//     moves between waves until the end, where the two key lanes of a row wave combine in lane order (fp32).
 //   * Transposed contractions on v_mfma_f32_16x16x32_bf16:  S^T = K Q^T  (M = tokens, N = rows, K = head dim) and
 //     O^T = V^T P^T  (M = head dim, N = rows, K = tokens). A lane then owns one query row per N-tile, so the online
 //     softmax max is two xor-shuffles and the row sum stays lane-local until the end. The P^T operand is the lane's
@@ -15,29 +18,39 @@
 //     moves between lanes.
 //   * K tiles live in LDS as [token][D] with an XOR swizzle of the 16-byte chunks (conflict-free 16-row reads);
 //     V pages are stored token-minor ([D][16] per page) in HBM, so the V^T operand is two 8-byte LDS reads.
-//   * A split's tiles are processed in stages of LANES = 4 tiles: the page ids of the whole split are read once
-//     into LDS, then every K/V load of a stage is issued at once, straight from global memory into LDS
-//     (global_load_lds_dwordx4; no staging registers). Tile j of a split belongs to tile lane j % 4; the compute waves
-//     of a row group are (N-tile, lane) pairs, each keeps its own online softmax, and the 4 lanes are combined in
-//     lane order at the end.
+//   * Stages of 2 tiles stream straight from global memory into LDS (global_load_lds_dwordx4; no staging
+//     registers) into two alternating buffers: stage st + 1 is in flight while stage st is computed, with one
+//     workgroup barrier per stage. A stage's page ids are read one stage ahead.
+//   * Grid order is XCD-aware: consecutive units go to different XCDs (ragged batches balance), the row groups of
+//     one unit to the same XCD (their repeated K/V reads hit its L2).
 //   * Keys are tiled by absolute position (window rows take the positions after the prefix); the split size and
-//     the tile -> split -> lane assignment depend only on the capacity max_kv_len and on fixed constants, never on
-//     W, the prefix length or the row grouping, and every combine runs in a fixed order. Results therefore do not
+//     the tile -> split -> key lane assignment depend only on the capacity max_kv_len and on fixed constants, never
+//     on W, the prefix length or the row grouping, and every combine runs in a fixed order. Results therefore do not
 //     depend on where a key comes from or on how many rows are in the window: a verify row reproduces the AR step
 //     of the same token bit for bit. With several splits, the normalized partial O (bf16) and (m, l) (fp32) of each
 //     split go to the caller's workspace and the merge kernel combines the valid splits of every row.
 #include "gss_common.h"
 
+#include <type_traits>
+
 namespace {
 
 constexpr int PAGE = 16;
 constexpr int TILE = 64;        // KV tokens per tile (4 pages)
-constexpr int LANES = 4;        // tiles per stage; tile j of a split goes to lane j % LANES
-constexpr int NTG = 3;          // query N-tiles (16 rows) per workgroup
-constexpr int NTHREADS = 64 * 2 * LANES;  // a wave per (tile lane, key half): 8 waves, 2 per SIMD
+constexpr int KL = 2;           // key lanes: tile j of a split is scored by the waves of lane j % KL
+constexpr int RW_MAX = 4;       // row waves per workgroup: <= 8 waves, 2 per SIMD
+constexpr int NGW_MAX = 3;      // N-tiles (16 query rows) per row wave
 constexpr int MAX_TPS = 256;    // tiles per split (page ids of a split in LDS: 4 * MAX_TPS ints)
 constexpr int MAX_SPLIT = 256;
 constexpr float LOG2E = 1.4426950408889634f;
+// a row's reference max may trail its running max by up to this (log2 domain): P^T <= 2^8, O and l stay far from
+// fp32 overflow, and the rescale of O runs only when a max jumps by more
+constexpr float RESCALE_SLACK = 8.f;
+// the row-group kernel (small batches): stages of RG_LANES tiles, a wave per (tile lane, key half), RG_NTG N-tiles
+// per workgroup
+constexpr int RG_LANES = 4;
+constexpr int RG_NTG = 3;
+constexpr int RG_THREADS = 64 * 2 * RG_LANES;
 
 typedef __attribute__((address_space(1))) void gvoid_t;  // global memory (direct-to-LDS load source)
 typedef __attribute__((address_space(3))) void lvoid_t;  // LDS (its destination)
@@ -53,22 +66,35 @@ struct AttnParams {
   uint16_t* out;
   uint16_t* ws_o;  // [bs, Hkv, n_split, R, D] bf16: O / l of each split
   float* ws_ml;    // [bs, Hkv, R, n_split, 2]:      (m, l) of each split (log2 domain max, sum)
-  int pt_stride, prefix_extra, W, n_causal, Hq, Hkv, G, R, n_split, S8, tps;
+  int pt_stride, prefix_extra, W, n_causal, Hq, Hkv, G, R, n_split, RW, TPG, RG, n_units, tps;
   float scale_log2;
 };
 
 template <int D>
 struct Lds {
   static constexpr int TILE_EL = TILE * D;          // elements of one K (or V) tile
-  static constexpr int V_OFF = LANES * TILE_EL;     // K stage [LANES][TILE][D] swizzled, then V [LANES][4][D][16]
-  static constexpr int BYTES = 2 * LANES * TILE_EL * 2;         // the K/V stage
-  static constexpr int MAX_BYTES = NTHREADS / 64 * NTG * 16 * 4;  // row-max exchange [waves][NG][16] after it
+  static constexpr int STAGE_EL = 2 * KL * TILE_EL;  // a stage buffer: K [KL][TILE][D] swizzled, V [KL][4][D][16]
+  static constexpr int BUF_BYTES = 2 * STAGE_EL * 2;  // two stage buffers (bytes)
+  static constexpr int TOTAL = BUF_BYTES + 4 * MAX_TPS * 4;  // then the split's page ids (4 pages per tile)
+  // combine scratch (reuses the stage buffers): per (row wave, key lane >= 1, N-tile) O^T fp32 and (m, l) of 16 rows
+  static constexpr int SCR_FLOATS = (D / 16) * 256 + 32;
+  static_assert(RW_MAX * (KL - 1) * NGW_MAX * SCR_FLOATS * 4 <= BUF_BYTES, "combine scratch exceeds the buffers");
+  static_assert(TOTAL <= 160 * 1024, "LDS budget");
+};
+
+template <int D>
+struct LdsRG {
+  static constexpr int TILE_EL = TILE * D;          // elements of one K (or V) tile
+  static constexpr int V_OFF = RG_LANES * TILE_EL;     // K stage [RG_LANES][TILE][D] swizzled, then V [RG_LANES][4][D][16]
+  static constexpr int BYTES = 2 * RG_LANES * TILE_EL * 2;         // the K/V stage
+  static constexpr int MAX_BYTES = RG_THREADS / 64 * RG_NTG * 16 * 4;  // row-max exchange [waves][NG][16] after it
   static constexpr int TOTAL = BYTES + MAX_BYTES;
   // combine scratch (reuses the K/V stage): per (wave, N-tile) O as bf16 [DT][64 lanes] x 4 + l [16 rows]
   static constexpr int SCR_BYTES = (D / 16) * 64 * 8 + 16 * 4;
-  static_assert(NTHREADS / 64 * NTG * SCR_BYTES <= BYTES, "combine scratch exceeds the K/V stage");
+  static_assert(RG_THREADS / 64 * RG_NTG * SCR_BYTES <= BYTES, "combine scratch exceeds the K/V stage");
   static_assert(TOTAL <= 160 * 1024, "LDS budget");
 };
+
 
 template <int D>
 GSS_DEV int k_lds_index(int tok, int chunk) {
@@ -87,28 +113,386 @@ GSS_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// 2^x with one v_exp_f32 (libm's exp2f wraps it in a denormal range fix-up of five more instructions). Every
+// argument here is <= 0 (a score minus its running max) or -inf; results below 2^-126 flush to zero, far below the
+// resolution of the bf16 probabilities and the fp32 row sums they feed.
+GSS_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 GSS_DEV int valid_splits(int L, int W, int tps) {
   const int n_tiles = (L + W + TILE - 1) / TILE;
   return (n_tiles + tps - 1) / tps;
 }
 
-template <int D, int NG>
-__global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) {
+template <int D, int NGW>
+__global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams p) {
   constexpr int KS = D / 32;   // MFMA K-steps over the head dim
   constexpr int DT = D / 16;   // 16-row tiles of the head dim (O^T M-tiles)
   constexpr int CH = D / 8;    // 16-byte chunks per K row
   constexpr int TILE_EL = Lds<D>::TILE_EL;
   constexpr int TILE_INSTR = TILE * CH / 64;    // direct-load instructions per K (or V) tile
-  constexpr int STAGE_INSTR = LANES * TILE_INSTR;
+  constexpr int STAGE_INSTR = 2 * KL * TILE_INSTR;  // K and V of the KL tiles of a stage
   constexpr int PAGE_INSTR = PAGE * CH / 64;    // instructions per (page, head) block of K (or V)
-  constexpr int NW = NTHREADS / 64;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+
+  // Grid order: workgroups are dealt to the 8 XCDs round-robin by linear index. A unit u = (sequence, kv head,
+  // split), numbered split-fastest, runs as workgroups (u / 8) * 8 * RG + rg * 8 + u % 8 for its RG row groups: all
+  // of them on XCD u % 8, dispatched back to back (so they share that XCD's L2 for the unit's K/V), and consecutive
+  // units (the splits of one sequence) on different XCDs, so ragged sequences, whose late splits are empty, spread
+  // their work evenly over the XCDs.
+  const int r8 = blockIdx.x % (8 * p.RG);
+  const int u = blockIdx.x / (8 * p.RG) * 8 + r8 % 8, rg = r8 / 8;
+  if (u >= p.n_units) return;  // padding of the last group of 8 units
+  const int s = u % p.n_split, kvh = (u / p.n_split) % p.Hkv, b = u / (p.n_split * p.Hkv);
+  const int tid = threadIdx.x, lane = tid & 63, NW = blockDim.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kl = wv % KL, rw = wv / KL;                       // key lane, row wave
+  const int l16 = lane & 15, g4 = lane >> 4;
+  // committed prefix length; clamped to what the page-table row can address so every page-table read is in bounds
+  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.pt_stride * PAGE);
+  const int W = p.W, nc = p.n_causal;
+  const int n_tiles = (L + W + TILE - 1) / TILE;
+  const int t_beg = s * p.tps, t_end = min(n_tiles, t_beg + p.tps);
+  if (t_beg >= t_end) return;  // no key of this sequence in this split (the merge counts only valid splits)
+  const int32_t* pt = p.page_table + static_cast<int64_t>(b) * p.pt_stride;
+  const int64_t head_stride = static_cast<int64_t>(PAGE) * D;          // elements per (page, kv head) block
+  const int64_t win_base = static_cast<int64_t>(b) * W * p.Hkv + kvh;  // window row j: (win_base + j*Hkv)*D
+
+  // ---- this wave's query fragments (the B operand of S^T = K Q^T), in registers for the whole kernel: N-tiles
+  // nt0 .. nt0 + ng - 1 (ng <= NGW, wave-uniform) of the sequence's R = G*W rows. Rows past R have zero queries and
+  // are never written; N-tiles g >= ng are skipped (never computed).
+  const int tb_base = p.TPG / p.RW, tb_extra = p.TPG % p.RW;
+  const int ng = tb_base + (rw < tb_extra ? 1 : 0);
+  const int nt0 = rg * p.TPG + rw * tb_base + min(rw, tb_extra);
+  bf16x8_t qf[NGW][KS];
+#pragma unroll
+  for (int g = 0; g < NGW; ++g) {
+    const int n = (nt0 + g) * 16 + l16;
+    const int nn = n < p.R ? n : 0;  // padding rows read row 0 (in bounds) and are zeroed
+    const uint16_t* qrow = p.q + ((static_cast<int64_t>(b) * W + nn / p.G) * p.Hq + kvh * p.G + nn % p.G) * D;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      qf[g][ks] = (g < ng && n < p.R) ? *reinterpret_cast<const bf16x8_t*>(qrow + ks * 32 + g4 * 8) : bf16x8_t{};
+  }
+
+  // ---- the split's page ids -> LDS, once (their loads are in flight with the query loads above). Stage loads then
+  // take their page ids from LDS, so the only vector-memory loads in flight during the stage loop are the K/V stage
+  // loads themselves, and the wait for one stage never waits for another's.
+  int* spages = reinterpret_cast<int*>(reinterpret_cast<char*>(smem) + Lds<D>::BUF_BYTES);
+  for (int i = tid; i < (t_end - t_beg) * (TILE / PAGE); i += blockDim.x) {
+    const int pos = t_beg * TILE + i * PAGE;
+    spages[i] = pos < L ? pt[pos / PAGE] : 0;
+  }
+  // queries pre-scaled by scale * log2(e) (fp32 product rounded to bf16), so the MFMA yields log2-domain scores
+#pragma unroll
+  for (int g = 0; g < NGW; ++g)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4_t u = __builtin_bit_cast(u32x4_t, qf[g][ks]);
+      u32x4_t r;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        r[e] = cvt_pk_bf16(__uint_as_float(u[e] << 16) * p.scale_log2,
+                           __uint_as_float(u[e] & 0xffff0000u) * p.scale_log2);
+      qf[g][ks] = __builtin_bit_cast(bf16x8_t, r);
+    }
+  __syncthreads();
+
+  // ---- stage loads, global -> LDS directly (global_load_lds_dwordx4: lane i of an instruction writes the 16 bytes
+  // at the instruction's LDS base + 16 i). A stage is KL tiles, held in buffer st % 2 as K [KL][TILE][D] (XOR-swizzled
+  // 16-byte chunks) then V [KL][4 pages][D][16]. Every instruction covers 64 chunks of one (page, head) block, so its
+  // page id is wave-uniform. Chunks of positions >= L are not loaded.
+  auto issue_stage = [&](int st) {
+    uint16_t* buf = smem + (st & 1) * Lds<D>::STAGE_EL;
+    // lane j holds page j of the stage (one LDS read per lane); readlane broadcasts the one an instruction needs
+    const int pgv = lane < KL * (TILE / PAGE) && st * KL * (TILE / PAGE) + lane < (t_end - t_beg) * (TILE / PAGE)
+                        ? spages[st * KL * (TILE / PAGE) + lane]
+                        : 0;
+    for (int ii = wv; ii < STAGE_INSTR; ii += NW) {
+      const bool is_v = ii >= KL * TILE_INSTR;
+      const int iv = is_v ? ii - KL * TILE_INSTR : ii;
+      const int tl = iv / TILE_INSTR, ib = iv % TILE_INSTR;
+      const int t = t_beg + st * KL + tl;
+      if (t >= t_end) continue;
+      const int pblk = ib / PAGE_INSTR, pat = ib % PAGE_INSTR;
+      const int pos0 = t * TILE + pblk * PAGE;  // first position of the page
+      const int kr = pat * 64 + lane;
+      int off;
+      bool in_prefix;
+      if (is_v) {
+        const int vd = kr >> 1, vh = (kr & 1) ^ ((vd >> 3) & 1);
+        off = vd * PAGE + vh * 8;
+        in_prefix = pos0 + vh * 8 < L;
+      } else {
+        const int ktok = kr / CH;
+        off = ktok * D + ((kr % CH) ^ (ktok & (CH - 1))) * 8;
+        in_prefix = pos0 + ktok < L;
+      }
+      const int64_t page = __builtin_amdgcn_readlane(pgv, tl * (TILE / PAGE) + pblk);
+      const uint16_t* base = (is_v ? p.v_pages : p.k_pages) + (page * p.Hkv + kvh) * head_stride;
+      if (in_prefix)
+        __builtin_amdgcn_global_load_lds((gvoid_t*)(base + off),
+                                         (lvoid_t*)(buf + (is_v ? KL * TILE_EL : 0) + iv * 512), 16, 0, 0);
+    }
+  };
+  // Tiles that reach past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
+  // and the V chunk that straddles L keeps only its prefix tokens.
+  auto fix_stage = [&](int st) {
+    uint16_t* lds_k = smem + (st & 1) * Lds<D>::STAGE_EL;
+    uint16_t* lds_v = lds_k + KL * TILE_EL;
+    const int ts = t_beg + st * KL, te = min(t_end, ts + KL);
+    const int t0 = max(ts, L / TILE);
+    if (t0 >= te) return false;
+    for (int c = tid; c < (te - t0) * TILE * CH; c += blockDim.x) {  // K chunks of the boundary tiles
+      const int t = t0 + c / (TILE * CH), r = c % (TILE * CH), tok = r / CH, part = r % CH;
+      const int pos = t * TILE + tok;
+      if (pos < L) continue;
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (pos < L + W)
+        v = *reinterpret_cast<const u32x4_t*>(p.k_win + (win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D +
+                                              part * 8);
+      *reinterpret_cast<u32x4_t*>(&lds_k[(t - ts) * TILE_EL + k_lds_index<D>(tok, part)]) = v;
+    }
+    for (int c = tid; c < (te - t0) * TILE * CH; c += blockDim.x) {  // V chunks of the boundary tiles
+      const int t = t0 + c / (TILE * CH), r = c % (TILE * CH);
+      const int pi = r / (2 * D), r2 = r % (2 * D), d = r2 >> 1, h = r2 & 1;
+      const int first = t * TILE + pi * PAGE + h * 8;  // absolute position of the chunk's first token
+      if (first + 8 <= L) continue;
+      uint16_t* dst = &lds_v[(t - ts) * TILE_EL + v_lds_index(pi, d, h, D)];
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      const int keep = L - first;  // tokens of the chunk inside the prefix (loaded from the page)
+      if (keep > 0) {
+        v = *reinterpret_cast<const u32x4_t*>(dst);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = (2 * e < keep) ? 0x0000ffffu : 0u, hi = (2 * e + 1 < keep) ? 0xffff0000u : 0u;
+          v[e] &= (lo | hi);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int pos = first + e;
+        if (pos >= L && pos < L + W) {
+          const uint32_t x = p.v_win[(win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D + d];
+          v[e >> 1] |= (e & 1) ? (x << 16) : x;
+        }
+      }
+      *reinterpret_cast<u32x4_t*>(dst) = v;
+    }
+    return true;
+  };
+
+  // ---- online softmax, private to the wave: key lane kl takes tiles t_beg + kl, t_beg + kl + KL, ... of the split,
+  // each whole (4 m-tiles of 16 keys), for its ng N-tiles. Scores come out of the MFMA in the log2 domain (the
+  // queries are pre-scaled). Each row keeps a reference max m that trails its running max by at most RESCALE_SLACK,
+  // and P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more than the slack
+  // (rare after the first tiles) does the wave move the references and rescale O and l. Row maxima: 16 values per
+  // lane, then two xor-shuffles over the lanes of a row. P^T is packed to bf16 in the lane that scored it, and
+  // O^T += V^T P^T over 2 K-steps of 32 keys.
+  floatx4_t o[NGW][DT];
+  float m_run[NGW], l_run[NGW];
+#pragma unroll
+  for (int g = 0; g < NGW; ++g) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[g][dt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    m_run[g] = -INFINITY;
+    l_run[g] = 0.f;
+  }
+  const int hsw = (l16 >> 3) & 1;  // the V half swap of head dims d with bit 3 set (d = dt*16 + l16)
+  const int vrd = ((g4 >> 1) ^ hsw) * 8 + (g4 & 1) * 4;
+
+  const int n_stages = (t_end - t_beg + KL - 1) / KL;
+  issue_stage(0);
+  for (int st = 0; st < n_stages; ++st) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of stage st
+    __syncthreads();  // every wave's loads of stage st have landed; every wave is done with stage st - 1's buffer
+    if (fix_stage(st)) __syncthreads();  // block-uniform condition
+    if (st + 1 < n_stages) issue_stage(st + 1);  // stream stage st + 1 into the other buffer while st is computed
+    const int tb = (t_beg + st * KL + kl) * TILE;
+    if (tb >= t_end * TILE) continue;  // wave-uniform: this key lane has no tile in the last stage
+    const uint16_t* tk = smem + (st & 1) * Lds<D>::STAGE_EL + kl * TILE_EL;
+    const uint16_t* tv = tk + KL * TILE_EL;
+    floatx4_t sacc[NGW][4];
+#pragma unroll
+    for (int g = 0; g < NGW; ++g)
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) sacc[g][mt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) {  // one K fragment live at a time; it feeds the ng N-tiles
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&tk[k_lds_index<D>(mt * 16 + l16, ks * 4 + g4)]);
+#pragma unroll
+        for (int g = 0; g < NGW; ++g)
+          if (g < ng) sacc[g][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[g][ks], sacc[g][mt], 0, 0, 0);
+      }
+    }
+    if (tb + TILE > L) {  // keys past the prefix: the window mask (wave-uniform branch)
+#pragma unroll
+      for (int g = 0; g < NGW; ++g) {
+        const int n = (nt0 + g) * 16 + l16;
+        const int roww = (n < p.R ? n : 0) / p.G;  // the row's window index
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int pos = tb + mt * 16 + g4 * 4 + i;
+            const int wj = pos - L;
+            const bool vis = pos < L || (wj < W && (roww >= nc || wj <= roww));
+            if (!vis) sacc[g][mt][i] = -INFINITY;
+          }
+      }
+    }
+    // row maxima and reference moves of every N-tile, then per K-step kk (keys of m-tiles 2kk in P^T slots 0..3,
+    // 2kk+1 in slots 4..7): the P^T operands of all N-tiles, then each V^T fragment read once for all of them
+    float m_use[NGW], ls[NGW];
+#pragma unroll
+    for (int g = 0; g < NGW; ++g) {
+      m_use[g] = 0.f;
+      ls[g] = 0.f;
+      if (g >= ng) continue;  // wave-uniform
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        mx = fmaxf(mx, fmaxf(fmaxf(sacc[g][mt][0], sacc[g][mt][1]), fmaxf(sacc[g][mt][2], sacc[g][mt][3])));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // the row's reference moves only when its max exceeds it by more than the slack (or on its first visible
+      // tile, m_run = -inf); a tile whose keys are all masked (mx = -inf) never moves it
+      if (__any(mx > m_run[g] + RESCALE_SLACK)) {  // wave-uniform: rescale O and l of the rows that moved
+        const float m_new = mx > m_run[g] + RESCALE_SLACK ? mx : m_run[g];
+        // 1 for rows that keep their reference (also -inf: no visible key yet, where -inf - -inf would be NaN),
+        // 0 on a row's first visible tile
+        const float alpha = m_new == m_run[g] ? 1.f : fast_exp2(m_run[g] - m_new);
+        m_run[g] = m_new;
+        l_run[g] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * alpha;
+      }
+      m_use[g] = m_run[g] == -INFINITY ? 0.f : m_run[g];  // a row with no visible key yet: P = 0
+    }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8_t pb[NGW];
+#pragma unroll
+      for (int g = 0; g < NGW; ++g) {
+        if (g >= ng) continue;
+        uint32_t pk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const floatx4_t& sv = sacc[g][2 * kk + (j >> 1)];
+          const float p0 = fast_exp2(sv[(2 * j) & 3] - m_use[g]);
+          const float p1 = fast_exp2(sv[(2 * j + 1) & 3] - m_use[g]);
+          ls[g] += p0 + p1;
+          pk[j] = cvt_pk_bf16(p0, p1);
+        }
+        pb[g] = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int d = dt * 16 + l16;
+        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * kk) * D + d) * PAGE + vrd]);
+        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * kk + 1) * D + d) * PAGE + vrd]);
+        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, u32x4_t{v0[0], v0[1], v1[0], v1[1]});
+#pragma unroll
+        for (int g = 0; g < NGW; ++g)
+          if (g < ng) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g], o[g][dt], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < NGW; ++g) l_run[g] += ls[g];
+  }
+
+  // ---- combine the KL key lanes of each row wave in lane order (fp32, through LDS), normalize, write.
+#pragma unroll
+  for (int g = 0; g < NGW; ++g) {
+    l_run[g] += __shfl_xor(l_run[g], 16, 64);
+    l_run[g] += __shfl_xor(l_run[g], 32, 64);
+  }
+  __syncthreads();  // every wave is done with the stage buffers: reuse them as scratch
+  float* scr = reinterpret_cast<float*>(smem);
+  // slot of (row wave, key lane k >= 1, N-tile g): O^T [DT][64 lanes] x 4, then m [16 rows], l [16 rows]
+  auto slot = [&](int k, int g) {
+    return scr + static_cast<size_t>((rw * (KL - 1) + k - 1) * NGW + g) * Lds<D>::SCR_FLOATS;
+  };
+  if (kl != 0) {
+#pragma unroll
+    for (int g = 0; g < NGW; ++g) {
+      if (g >= ng) continue;
+      float* sl = slot(kl, g);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) reinterpret_cast<floatx4_t*>(sl)[dt * 64 + lane] = o[g][dt];
+      if (g4 == 0) {
+        sl[DT * 256 + l16] = m_run[g];
+        sl[DT * 256 + 16 + l16] = l_run[g];
+      }
+    }
+  }
+  __syncthreads();
+  if (kl != 0) return;
+#pragma unroll
+  for (int g = 0; g < NGW; ++g) {
+    if (g >= ng) continue;
+    const int n = (nt0 + g) * 16 + l16;
+    float M = m_run[g];
+#pragma unroll
+    for (int k = 1; k < KL; ++k) M = fmaxf(M, slot(k, g)[DT * 256 + l16]);
+    const float Mu = M == -INFINITY ? 0.f : M;
+    const float a0 = fast_exp2(m_run[g] - Mu);
+    float lc = l_run[g] * a0;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * a0;
+#pragma unroll
+    for (int k = 1; k < KL; ++k) {
+      const float* sl = slot(k, g);
+      const float ak = fast_exp2(sl[DT * 256 + l16] - Mu);
+      lc += sl[DT * 256 + 16 + l16] * ak;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[g][dt] += reinterpret_cast<const floatx4_t*>(sl)[dt * 64 + lane] * ak;
+    }
+    if (n >= p.R) continue;
+    const float inv = lc > 0.f ? 1.f / lc : 0.f;
+    uint16_t* orow;
+    if (p.n_split == 1) {
+      orow = p.out + ((static_cast<int64_t>(b) * W + n / p.G) * p.Hq + kvh * p.G + n % p.G) * D;
+    } else {
+      const int64_t rowid = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.R + n;  // (m, l): [bs, Hkv, R, n_split]
+      orow = p.ws_o + ((static_cast<int64_t>(b) * p.Hkv + kvh) * p.n_split + s) * p.R * D +
+             static_cast<int64_t>(n) * D;
+      if (g4 == 0) {
+        p.ws_ml[(rowid * p.n_split + s) * 2 + 0] = M;
+        p.ws_ml[(rowid * p.n_split + s) * 2 + 1] = lc;
+      }
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<u32x2_t*>(orow + dt * 16 + g4 * 4) =
+          u32x2_t{cvt_pk_bf16(o[g][dt][0] * inv, o[g][dt][1] * inv), cvt_pk_bf16(o[g][dt][2] * inv, o[g][dt][3] * inv)};
+  }
+}
+
+// Row-group kernel for small batches (bs * Hkv below the wide threshold), where the chip must be filled from few
+// key splits: the R rows are cut into row groups of up to RG_NTG N-tiles, each its own workgroup (the groups of a
+// unit share its K/V through the XCD's L2), 8 waves = (tile lane, key half) pairs over stages of RG_LANES tiles, one
+// running max per row shared by the waves through LDS, and the 8 partial (O, l) summed in wave order.
+template <int D, int NG>
+__global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams p) {
+  constexpr int KS = D / 32;   // MFMA K-steps over the head dim
+  constexpr int DT = D / 16;   // 16-row tiles of the head dim (O^T M-tiles)
+  constexpr int CH = D / 8;    // 16-byte chunks per K row
+  constexpr int TILE_EL = LdsRG<D>::TILE_EL;
+  constexpr int TILE_INSTR = TILE * CH / 64;    // direct-load instructions per K (or V) tile
+  constexpr int STAGE_INSTR = RG_LANES * TILE_INSTR;
+  constexpr int PAGE_INSTR = PAGE * CH / 64;    // instructions per (page, head) block of K (or V)
+  constexpr int NW = RG_THREADS / 64;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* lds_k = smem;
-  uint16_t* lds_v = smem + Lds<D>::V_OFF;
+  uint16_t* lds_v = smem + LdsRG<D>::V_OFF;
 
-  const int s = blockIdx.x % p.S8, rg = blockIdx.x / p.S8;  // split, row group
-  if (s >= p.n_split) return;                                 // XCD-alignment padding
-  const int kvh = blockIdx.y, b = blockIdx.z;
+  // grid order: as attn_split_kernel (units spread over the XCDs, the row groups of a unit on one XCD)
+  const int r8 = blockIdx.x % (8 * p.RG);
+  const int u = blockIdx.x / (8 * p.RG) * 8 + r8 % 8, rg = r8 / 8;
+  if (u >= p.n_units) return;  // padding of the last group of 8 units
+  const int s = u % p.n_split, kvh = (u / p.n_split) % p.Hkv, b = u / (p.n_split * p.Hkv);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kq = wv >> 1, half = wv & 1;                      // tile lane, key half (32 keys) of this wave
@@ -153,8 +537,8 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
   const int vr = kr % (2 * D), vd = vr >> 1, vh = (vr & 1) ^ ((vd >> 3) & 1);
   const int voff = vd * PAGE + vh * 8;
   auto stage_pages = [&](int st) {
-    const int pos = (t_beg + st * LANES) * TILE + lane * PAGE;
-    return (lane < LANES * (TILE / PAGE) && pos < L) ? pt[pos / PAGE] : 0;
+    const int pos = (t_beg + st * RG_LANES) * TILE + lane * PAGE;
+    return (lane < RG_LANES * (TILE / PAGE) && pos < L) ? pt[pos / PAGE] : 0;
   };
   auto issue_stage = [&](int st, int pgv) {
 #pragma unroll 4
@@ -162,7 +546,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
       const int ii = i * NW + wv;
       const bool is_v = ii >= STAGE_INSTR;
       const int iv = is_v ? ii - STAGE_INSTR : ii;
-      const int t = t_beg + st * LANES + iv / TILE_INSTR;
+      const int t = t_beg + st * RG_LANES + iv / TILE_INSTR;
       if (t >= t_end) continue;
       const int pblk = iv / PAGE_INSTR;                         // page of the stage (tile * 4 + page in tile)
       const int pos0 = t * TILE + (pblk % (TILE / PAGE)) * PAGE;  // first position of that page
@@ -171,16 +555,16 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
       const bool in_prefix = pos0 + PAGE <= L || (is_v ? pos0 + vh * 8 < L : pos0 + ktok < L);
       if (in_prefix)
         __builtin_amdgcn_global_load_lds((gvoid_t*)(base + (is_v ? voff : koff)),
-                                         (lvoid_t*)(smem + (is_v ? Lds<D>::V_OFF : 0) + iv * 512), 16, 0, 0);
+                                         (lvoid_t*)(smem + (is_v ? LdsRG<D>::V_OFF : 0) + iv * 512), 16, 0, 0);
     }
   };
   // Tiles that reach past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
   // and the V chunk that straddles L keeps only its prefix tokens.
   auto fix_stage = [&](int st) {
-    const int ts = t_beg + st * LANES, te = min(t_end, ts + LANES);
+    const int ts = t_beg + st * RG_LANES, te = min(t_end, ts + RG_LANES);
     const int t0 = max(ts, L / TILE);
     if (t0 >= te) return false;
-    for (int c = tid; c < (te - t0) * TILE * CH; c += NTHREADS) {  // K chunks of the boundary tiles
+    for (int c = tid; c < (te - t0) * TILE * CH; c += RG_THREADS) {  // K chunks of the boundary tiles
       const int t = t0 + c / (TILE * CH), r = c % (TILE * CH), tok = r / CH, part = r % CH;
       const int pos = t * TILE + tok;
       if (pos < L) continue;
@@ -190,7 +574,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
                                               part * 8);
       *reinterpret_cast<u32x4_t*>(&lds_k[(t - ts) * TILE_EL + k_lds_index<D>(tok, part)]) = v;
     }
-    for (int c = tid; c < (te - t0) * TILE * CH; c += NTHREADS) {  // V chunks of the boundary tiles
+    for (int c = tid; c < (te - t0) * TILE * CH; c += RG_THREADS) {  // V chunks of the boundary tiles
       const int t = t0 + c / (TILE * CH), r = c % (TILE * CH);
       const int pi = r / (2 * D), r2 = r % (2 * D), d = r2 >> 1, h = r2 & 1;
       const int first = t * TILE + pi * PAGE + h * 8;  // absolute position of the chunk's first token
@@ -224,7 +608,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
   // N-tiles, the waves exchange their row maxima through LDS, and all of them rescale (from the second stage on)
   // and accumulate against the same running max. The 8 partial (O, l) of the workgroup are then on one scale and
   // combine by plain sums in a fixed order. Every K and V fragment read from LDS feeds the MFMAs of all NG N-tiles.
-  float* smax = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + Lds<D>::BYTES);  // [NW][NG][16]
+  float* smax = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + LdsRG<D>::BYTES);  // [NW][NG][16]
   floatx4_t o[NG][DT];
   float m_run[NG], l_run[NG];
 #pragma unroll
@@ -239,7 +623,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
   const int hsw = (l16 >> 3) & 1;  // the V half swap of head dims d with bit 3 set (d = dt*16 + l16)
   const int vrd = ((g4 >> 1) ^ hsw) * 8 + (g4 & 1) * 4;
 
-  const int n_stages = (t_end - t_beg + LANES - 1) / LANES;
+  const int n_stages = (t_end - t_beg + RG_LANES - 1) / RG_LANES;
   int pgv = stage_pages(0);
   for (int st = 0; st < n_stages; ++st) {
     if (st > 0) __syncthreads();  // the previous stage's compute is done with LDS
@@ -248,7 +632,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (fix_stage(st)) __syncthreads();  // block-uniform condition
-    const int tb = (t_beg + st * LANES + kq) * TILE;
+    const int tb = (t_beg + st * RG_LANES + kq) * TILE;
     const bool has_tile = tb < t_end * TILE;  // wave-uniform
     floatx4_t sacc[NG][2];
 #pragma unroll
@@ -304,7 +688,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
       const float m_new = fmaxf(m_run[g], mx * p.scale_log2);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       if (st > 0) {  // rescale to the new running max (the first stage starts from zero)
-        const float alpha = exp2f(m_run[g] - m_use);
+        const float alpha = fast_exp2(m_run[g] - m_use);
         l_run[g] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * alpha;
@@ -316,8 +700,8 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
         uint32_t pk[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float p0 = exp2f(__builtin_fmaf(sacc[g][j >> 1][(2 * j) & 3], p.scale_log2, nm));
-          const float p1 = exp2f(__builtin_fmaf(sacc[g][j >> 1][(2 * j + 1) & 3], p.scale_log2, nm));
+          const float p0 = fast_exp2(__builtin_fmaf(sacc[g][j >> 1][(2 * j) & 3], p.scale_log2, nm));
+          const float p1 = fast_exp2(__builtin_fmaf(sacc[g][j >> 1][(2 * j + 1) & 3], p.scale_log2, nm));
           ls += p0 + p1;
           pk[j] = cvt_pk_bf16(p0, p1);
         }
@@ -347,7 +731,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
   char* scr = reinterpret_cast<char*>(smem);
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
-    char* slot = scr + (wv * NG + g) * Lds<D>::SCR_BYTES;
+    char* slot = scr + (wv * NG + g) * LdsRG<D>::SCR_BYTES;
     u32x2_t* so = reinterpret_cast<u32x2_t*>(slot);
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
@@ -361,7 +745,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
     float lc = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const char* slot = scr + (w * NG + g) * Lds<D>::SCR_BYTES;
+      const char* slot = scr + (w * NG + g) * LdsRG<D>::SCR_BYTES;
       const u32x2_t u = reinterpret_cast<const u32x2_t*>(slot)[dt * 64 + lane];
       acc += floatx4_t{__uint_as_float(u[0] << 16), __uint_as_float(u[0] & 0xffff0000u), __uint_as_float(u[1] << 16),
                        __uint_as_float(u[1] & 0xffff0000u)};
@@ -390,6 +774,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) window_attn_kernel(AttnParams p) 
         u32x2_t{cvt_pk_bf16(acc[0] * inv, acc[1] * inv), cvt_pk_bf16(acc[2] * inv, acc[3] * inv)};
   }
 }
+
 
 // Combine the valid splits of each (sequence, kv head, row): block = one query row, 256 threads = (D/2 dim pairs) x
 // (SG split groups). All loads are issued in one round: the prefix length, the row's (m, l) of every split (stored
@@ -466,6 +851,7 @@ __global__ void __launch_bounds__(256) window_attn_merge(AttnParams p) {
 // (short splits fill the chip); a large batch gets few long splits, which keeps the partial traffic and the merge
 // small (32 ragged sequences of up to 12K keys: 8 splits of 25 tiles, 1.8x faster than 4 splits of 49).
 int g_target_wgs = 512, g_min_tiles = 4;
+int g_wide_min = 16;  // batches with bs * Hkv >= this run the wide kernel (gss_attn_set_wide_min)
 
 int attn_plan(int bs, int Hkv, int max_kv_len, int* n_split, int* tps) {
   const int tiles = (max(max_kv_len, 0) + TILE + TILE - 1) / TILE;
@@ -491,25 +877,47 @@ int validate(int bs, int W, int Hq, int Hkv, int D, int page) {
 }
 
 template <int D>
-int launch_d(const AttnParams& p, int bs, int NT, hipStream_t st) {
-  static bool lds_attr_set = false;  // allow the dynamic LDS beyond the default 64 KB (set once, before use)
-  if (!lds_attr_set) {
-    const void* fns[] = {reinterpret_cast<const void*>(&window_attn_kernel<D, 1>),
-                         reinterpret_cast<const void*>(&window_attn_kernel<D, 2>),
-                         reinterpret_cast<const void*>(&window_attn_kernel<D, 3>)};
-    for (const void* f : fns)
+int set_lds_limits() {
+  static bool done = false;  // allow the dynamic LDS beyond the default 64 KB (set once, before use)
+  if (!done) {
+    const void* wide[] = {reinterpret_cast<const void*>(&attn_split_kernel<D, 2>),
+                          reinterpret_cast<const void*>(&attn_split_kernel<D, 3>)};
+    for (const void* f : wide)
       if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, Lds<D>::TOTAL) != hipSuccess)
         return GSS_ERR_LAUNCH;
-    lds_attr_set = true;
+    const void* rg[] = {reinterpret_cast<const void*>(&attn_rowgroup_kernel<D, 1>),
+                        reinterpret_cast<const void*>(&attn_rowgroup_kernel<D, 2>),
+                        reinterpret_cast<const void*>(&attn_rowgroup_kernel<D, 3>)};
+    for (const void* f : rg)
+      if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, LdsRG<D>::TOTAL) != hipSuccess)
+        return GSS_ERR_LAUNCH;
+    done = true;
   }
-  const int NG = min(NTG, NT), RG = (NT + NG - 1) / NG;
-  const dim3 grid(p.S8 * RG, p.Hkv, bs);
-  if (NG == 1)
-    hipLaunchKernelGGL((window_attn_kernel<D, 1>), grid, dim3(NTHREADS), Lds<D>::TOTAL, st, p);
-  else if (NG == 2)
-    hipLaunchKernelGGL((window_attn_kernel<D, 2>), grid, dim3(NTHREADS), Lds<D>::TOTAL, st, p);
-  else
-    hipLaunchKernelGGL((window_attn_kernel<D, 3>), grid, dim3(NTHREADS), Lds<D>::TOTAL, st, p);
+  return GSS_OK;
+}
+
+// ng: N-tiles per row wave (wide kernel) or per workgroup (row-group kernel)
+template <int D>
+int launch_d(const AttnParams& p, int bs, bool wide, int ng, hipStream_t st) {
+  if (set_lds_limits<D>() != GSS_OK) return GSS_ERR_LAUNCH;
+  const dim3 grid((p.n_units + 7) / 8 * 8 * p.RG);
+  if (wide) {
+    const dim3 block(64 * KL * p.RW);
+    constexpr size_t lds = Lds<D>::TOTAL;
+    // one N-tile per wave runs on the two-tile instantiation (only its first tile is computed)
+    if (ng <= 2)
+      hipLaunchKernelGGL((attn_split_kernel<D, 2>), grid, block, lds, st, p);
+    else
+      hipLaunchKernelGGL((attn_split_kernel<D, 3>), grid, block, lds, st, p);
+  } else {
+    constexpr size_t lds = LdsRG<D>::TOTAL;
+    if (ng == 1)
+      hipLaunchKernelGGL((attn_rowgroup_kernel<D, 1>), grid, dim3(RG_THREADS), lds, st, p);
+    else if (ng == 2)
+      hipLaunchKernelGGL((attn_rowgroup_kernel<D, 2>), grid, dim3(RG_THREADS), lds, st, p);
+    else
+      hipLaunchKernelGGL((attn_rowgroup_kernel<D, 3>), grid, dim3(RG_THREADS), lds, st, p);
+  }
   if (p.n_split > 1) hipLaunchKernelGGL((window_attn_merge<D>), dim3(p.R, p.Hkv, bs), dim3(256), 0, st, p);
   return gss_launch_status();
 }
@@ -545,7 +953,24 @@ int attn_entry(const void* q, const void* k_pages, const void* v_pages, const in
   p.R = p.G * W;
   rc = attn_plan(bs, Hkv, max_kv_len, &p.n_split, &p.tps);
   if (rc != GSS_OK) return rc;
-  p.S8 = (p.n_split + 7) / 8 * 8;
+  p.n_units = bs * Hkv * p.n_split;
+  // kernel: a function of the batch shape only (never of W), so every window size of one batch runs the same one
+  const bool wide = bs * Hkv >= g_wide_min;
+  const int NT = (p.R + 15) / 16;
+  int ng;
+  if (wide) {
+    // rows: NT N-tiles of 16 in RG row groups of TPG tiles, dealt to RW row waves (the first TPG % RW take one
+    // more): 1 -> one wave of 1, 9 (17-row window) -> 3,2,2,2, 17 -> groups of 12 (3,3,3,3) and 5 (padding past NT)
+    p.RW = min(RW_MAX, NT);
+    p.TPG = min(NT, RW_MAX * NGW_MAX);
+    ng = (p.TPG + p.RW - 1) / p.RW;
+    p.RG = (NT + p.TPG - 1) / p.TPG;
+  } else {
+    // row groups of ng <= RG_NTG N-tiles, one workgroup each
+    ng = min(RG_NTG, NT);
+    p.RW = p.TPG = 0;
+    p.RG = (NT + ng - 1) / ng;
+  }
   p.scale_log2 = scale * LOG2E;
   p.ws_o = nullptr;
   p.ws_ml = nullptr;
@@ -556,8 +981,7 @@ int attn_entry(const void* q, const void* k_pages, const void* v_pages, const in
     p.ws_ml = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                        static_cast<size_t>(bs) * Hkv * p.n_split * p.R * D * sizeof(uint16_t));
   }
-  const int NT = (p.R + 15) / 16;
-  return D == 128 ? launch_d<128>(p, bs, NT, st) : launch_d<64>(p, bs, NT, st);
+  return D == 128 ? launch_d<128>(p, bs, wide, ng, st) : launch_d<64>(p, bs, wide, ng, st);
 }
 
 }  // namespace
@@ -592,6 +1016,12 @@ extern "C" int gss_verify_attn(const void* q, const void* k_pages, const void* v
   return attn_entry(q, k_pages, v_pages, page_table, pt_stride, prefix_len, prefix_extra, k_win, v_win, out, bs, W,
                     W, Hq, Hkv, D, page, scale, max_kv_len, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gss_attn_set_wide_min(int bs_hkv) {
+  if (bs_hkv < 1) return GSS_ERR_ARG;
+  g_wide_min = bs_hkv;
+  return GSS_OK;
 }
 
 extern "C" int gss_attn_set_split_policy(int target_wgs, int min_tiles) {

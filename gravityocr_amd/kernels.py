@@ -8,6 +8,9 @@ import torch
 from ._lib import NormEpilogue, NormPrologue, check, lib
 
 PAGE = 16
+# the attention kernels' library defaults (gss_attn_set_split_policy, gss_attn_set_wide_min)
+ATTN_POLICY = (512, 4)
+ATTN_WIDE_MIN = 16
 
 
 def _stream():

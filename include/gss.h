@@ -78,6 +78,13 @@ int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_le
  * sizing workspaces, and keep it fixed while a cache is decoded (it is part of the key partition). */
 int gss_attn_set_split_policy(int target_wgs, int min_tiles);
 
+/* Kernel choice of both attention entry points: batches with bs * Hkv >= bs_hkv (default 16) run the wide kernel
+ * (one workgroup per key split for all query rows, double-buffered stages), smaller ones the row-group kernel (the
+ * rows of a split spread over up to ceil(R / 48) workgroups, which fills the chip from few splits). Process-wide
+ * and, like the split policy, part of how a batch's keys are combined: keep it fixed while a cache is decoded.
+ * No counterpart in the reference (a launch-shape knob of these kernels). */
+int gss_attn_set_wide_min(int bs_hkv);
+
 int gss_draft_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int pt_stride,
                    const int32_t* prefix_len, int prefix_extra, const void* k_win, const void* v_win, void* out,
                    int bs, int W, int n_causal, int Hq, int Hkv, int D, int page, float scale, int max_kv_len,

@@ -69,6 +69,7 @@ def test_entry_points_reject_bad_arguments_before_launch():
     assert L.gss_gemm_set_policy(0, 16, 1) == ARG
     assert L.gss_gemm_set_policy(12, 16, 9) == ARG
     assert L.gss_attn_set_split_policy(0, 2) == ARG
+    assert L.gss_attn_set_wide_min(0) == ARG
 
 
 REFERENCE_SIGNATURES = {

@@ -3,7 +3,7 @@
 Kernel-only workload: 1 sequence, 16 q / 2 kv heads, head_dim 128, committed prefix L in {1K, 4K, 8K, 16K} in
 16-token pages in a shuffled page order, 17 window rows (boundary token + 16 masks), Q/K/V ~ N(0,1)/sqrt(128),
 seed 1; draft mask (row 0 causal, rows 1.. bidirectional) and verify mask (causal). Tolerance: max |err| <=
-1e-2 * max |ref| (bf16 output). Unused cache slots hold NaN, so a read outside the committed prefix would show.
+1e-2 * max |ref| (bf16 output). Every case runs on both kernels (row-group and wide). Unused cache slots hold NaN, so a read outside the committed prefix would show.
 """
 import numpy as np
 import pytest
@@ -13,6 +13,17 @@ from oracle.attention import masked_attention, window_mask
 from tests.helpers import ATTN_REL, PAGE, rel_err, shuffled_page_table
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True, params=["rowgroup", "wide"])
+def attn_kernel(request):
+    """Every case runs through both attention kernels: the row-group kernel (small batches) and the wide kernel
+    (large batches), selected by the bs * Hkv threshold."""
+    from gravityocr_amd._lib import lib
+    from gravityocr_amd.kernels import ATTN_WIDE_MIN
+    assert lib().gss_attn_set_wide_min(1 << 30 if request.param == "rowgroup" else 1) == 0
+    yield request.param
+    assert lib().gss_attn_set_wide_min(ATTN_WIDE_MIN) == 0
 
 
 def run_case(dev, Ls, W, n_causal, Hq=16, Hkv=2, D=128, seed=1, max_kv_len=None, prefix_extra=0, verify=False,
@@ -105,15 +116,17 @@ def test_deterministic(cuda):
 
 @pytest.mark.parametrize("policy", [(1, 256), (4096, 1), (64, 9)])
 def test_split_policies(cuda, policy):
-    """One split (direct output), one tile per split (many partials), and 9-tile splits (three stages per split)."""
+    """One split (direct output), one tile per split (many partials, one key lane idle), and 9-tile splits (several
+    stages per split, the last one half full)."""
     from gravityocr_amd._lib import lib
+    from gravityocr_amd.kernels import ATTN_POLICY
     print(f"policy={policy}", flush=True)
     assert lib().gss_attn_set_split_policy(*policy) == 0
     try:
         run_case(cuda, [5000], 17, 1, seed=21)
         run_case(cuda, [5000, 17, 700], 17, 1, seed=22, verify=True, max_kv_len=6000)
     finally:
-        assert lib().gss_attn_set_split_policy(512, 4) == 0
+        assert lib().gss_attn_set_split_policy(*ATTN_POLICY) == 0
 
 
 def test_stale_workspace(cuda):
