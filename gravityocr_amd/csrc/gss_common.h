@@ -15,19 +15,18 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 GSS_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN), the rounding of torch's .to(torch.bfloat16).
-GSS_DEV uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
-}
-
-GSS_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+// Round-to-nearest-even fp32 -> bf16, the rounding of torch's .to(torch.bfloat16), in gfx950's conversion
+// instruction (v_cvt_pk_bf16_f32, one instruction per pair; NaN stays a quiet NaN).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 GSS_DEV uint32_t pack_bf16x2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
+
+GSS_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
+
+GSS_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
 GSS_DEV float wave_sum(float v) {
 #pragma unroll
