@@ -118,6 +118,67 @@ GSS_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
 // resolution of the bf16 probabilities and the fp32 row sums they feed.
 GSS_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Boundary tiles ts..te-1 of a stage held in LDS (tile t's K at lds_k + (t - ts) * TILE * D, V likewise), t0 the
+// first tile that reaches past the prefix L: window row j < W (position L + j) comes from k_win / v_win, positions
+// past L + W are zero, and the V chunk that straddles L keeps only its prefix tokens. The thread's first window
+// loads are issued before the LDS pass that clears everything past the prefix, so the whole fix costs about one
+// memory round trip; a workgroup barrier separates the clearing from the window writes, and the caller follows
+// with another before the tiles are read.
+template <int D>
+GSS_DEV void fix_boundary(uint16_t* lds_k, uint16_t* lds_v, int ts, int t0, int te, int L, int W,
+                          const uint16_t* k_win, const uint16_t* v_win, int64_t win_base, int Hkv, int tid,
+                          int nthr) {
+  constexpr int CH = D / 8, TILE_EL = TILE * D;
+  const int j0 = max(0, t0 * TILE - L), j1 = min(W, te * TILE - L);  // window rows inside these tiles
+  const int n_win = max(0, j1 - j0) * CH;                             // their 16-byte chunks (8 dims of a row)
+  auto win_addr = [&](int c) { return (win_base + static_cast<int64_t>(j0 + c / CH) * Hkv) * D + (c % CH) * 8; };
+  u32x4_t kw = {0u, 0u, 0u, 0u}, vw = {0u, 0u, 0u, 0u};
+  if (tid < n_win) {
+    kw = *reinterpret_cast<const u32x4_t*>(k_win + win_addr(tid));
+    vw = *reinterpret_cast<const u32x4_t*>(v_win + win_addr(tid));
+  }
+  for (int c = tid; c < (te - t0) * TILE * CH; c += nthr) {  // K chunks past the prefix -> 0
+    const int t = t0 + c / (TILE * CH), r = c % (TILE * CH), tok = r / CH, part = r % CH;
+    if (t * TILE + tok >= L)
+      *reinterpret_cast<u32x4_t*>(&lds_k[(t - ts) * TILE_EL + k_lds_index<D>(tok, part)]) = u32x4_t{0u, 0u, 0u, 0u};
+  }
+  for (int c = tid; c < (te - t0) * TILE * CH; c += nthr) {  // V tokens past the prefix -> 0
+    const int t = t0 + c / (TILE * CH), r = c % (TILE * CH);
+    const int pi = r / (2 * D), r2 = r % (2 * D), d = r2 >> 1, h = r2 & 1;
+    const int first = t * TILE + pi * PAGE + h * 8;  // absolute position of the chunk's first token
+    if (first + 8 <= L) continue;
+    uint16_t* dst = &lds_v[(t - ts) * TILE_EL + v_lds_index(pi, d, h, D)];
+    u32x4_t v = {0u, 0u, 0u, 0u};
+    const int keep = L - first;  // tokens of the chunk inside the prefix (loaded from the page)
+    if (keep > 0) {
+      v = *reinterpret_cast<const u32x4_t*>(dst);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = (2 * e < keep) ? 0x0000ffffu : 0u, hi = (2 * e + 1 < keep) ? 0xffff0000u : 0u;
+        v[e] &= (lo | hi);
+      }
+    }
+    *reinterpret_cast<u32x4_t*>(dst) = v;
+  }
+  __syncthreads();
+  for (int c = tid; c < n_win; c += nthr) {  // window rows -> K chunks and V columns
+    if (c != tid) {
+      kw = *reinterpret_cast<const u32x4_t*>(k_win + win_addr(c));
+      vw = *reinterpret_cast<const u32x4_t*>(v_win + win_addr(c));
+    }
+    const int pos = L + j0 + c / CH, part = c % CH;
+    const int t = pos / TILE, tok = pos % TILE;
+    *reinterpret_cast<u32x4_t*>(&lds_k[(t - ts) * TILE_EL + k_lds_index<D>(tok, part)]) = kw;
+    const int pi = tok / PAGE, h = (tok % PAGE) / 8, e0 = tok % 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = part * 8 + e;
+      lds_v[(t - ts) * TILE_EL + v_lds_index(pi, d, h, D) + e0] =
+          static_cast<uint16_t>((e & 1) ? (vw[e >> 1] >> 16) : (vw[e >> 1] & 0xffffu));
+    }
+  }
+}
+
 GSS_DEV int valid_splits(int L, int W, int tps) {
   const int n_tiles = (L + W + TILE - 1) / TILE;
   return (n_tiles + tps - 1) / tps;
@@ -238,46 +299,11 @@ __global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams
   // and the V chunk that straddles L keeps only its prefix tokens.
   auto fix_stage = [&](int st) {
     uint16_t* lds_k = smem + (st & 1) * Lds<D>::STAGE_EL;
-    uint16_t* lds_v = lds_k + KL * TILE_EL;
     const int ts = t_beg + st * KL, te = min(t_end, ts + KL);
     const int t0 = max(ts, L / TILE);
     if (t0 >= te) return false;
-    for (int c = tid; c < (te - t0) * TILE * CH; c += blockDim.x) {  // K chunks of the boundary tiles
-      const int t = t0 + c / (TILE * CH), r = c % (TILE * CH), tok = r / CH, part = r % CH;
-      const int pos = t * TILE + tok;
-      if (pos < L) continue;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (pos < L + W)
-        v = *reinterpret_cast<const u32x4_t*>(p.k_win + (win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D +
-                                              part * 8);
-      *reinterpret_cast<u32x4_t*>(&lds_k[(t - ts) * TILE_EL + k_lds_index<D>(tok, part)]) = v;
-    }
-    for (int c = tid; c < (te - t0) * TILE * CH; c += blockDim.x) {  // V chunks of the boundary tiles
-      const int t = t0 + c / (TILE * CH), r = c % (TILE * CH);
-      const int pi = r / (2 * D), r2 = r % (2 * D), d = r2 >> 1, h = r2 & 1;
-      const int first = t * TILE + pi * PAGE + h * 8;  // absolute position of the chunk's first token
-      if (first + 8 <= L) continue;
-      uint16_t* dst = &lds_v[(t - ts) * TILE_EL + v_lds_index(pi, d, h, D)];
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      const int keep = L - first;  // tokens of the chunk inside the prefix (loaded from the page)
-      if (keep > 0) {
-        v = *reinterpret_cast<const u32x4_t*>(dst);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = (2 * e < keep) ? 0x0000ffffu : 0u, hi = (2 * e + 1 < keep) ? 0xffff0000u : 0u;
-          v[e] &= (lo | hi);
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int pos = first + e;
-        if (pos >= L && pos < L + W) {
-          const uint32_t x = p.v_win[(win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D + d];
-          v[e >> 1] |= (e & 1) ? (x << 16) : x;
-        }
-      }
-      *reinterpret_cast<u32x4_t*>(dst) = v;
-    }
+    fix_boundary<D>(lds_k, lds_k + KL * TILE_EL, ts, t0, te, L, W, p.k_win, p.v_win, win_base, p.Hkv, tid,
+                    blockDim.x);
     return true;
   };
 
@@ -564,42 +590,7 @@ __global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams
     const int ts = t_beg + st * RG_LANES, te = min(t_end, ts + RG_LANES);
     const int t0 = max(ts, L / TILE);
     if (t0 >= te) return false;
-    for (int c = tid; c < (te - t0) * TILE * CH; c += RG_THREADS) {  // K chunks of the boundary tiles
-      const int t = t0 + c / (TILE * CH), r = c % (TILE * CH), tok = r / CH, part = r % CH;
-      const int pos = t * TILE + tok;
-      if (pos < L) continue;
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (pos < L + W)
-        v = *reinterpret_cast<const u32x4_t*>(p.k_win + (win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D +
-                                              part * 8);
-      *reinterpret_cast<u32x4_t*>(&lds_k[(t - ts) * TILE_EL + k_lds_index<D>(tok, part)]) = v;
-    }
-    for (int c = tid; c < (te - t0) * TILE * CH; c += RG_THREADS) {  // V chunks of the boundary tiles
-      const int t = t0 + c / (TILE * CH), r = c % (TILE * CH);
-      const int pi = r / (2 * D), r2 = r % (2 * D), d = r2 >> 1, h = r2 & 1;
-      const int first = t * TILE + pi * PAGE + h * 8;  // absolute position of the chunk's first token
-      if (first + 8 <= L) continue;
-      uint16_t* dst = &lds_v[(t - ts) * TILE_EL + v_lds_index(pi, d, h, D)];
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      const int keep = L - first;  // tokens of the chunk inside the prefix (loaded from the page)
-      if (keep > 0) {
-        v = *reinterpret_cast<const u32x4_t*>(dst);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t lo = (2 * e < keep) ? 0x0000ffffu : 0u, hi = (2 * e + 1 < keep) ? 0xffff0000u : 0u;
-          v[e] &= (lo | hi);
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int pos = first + e;
-        if (pos >= L && pos < L + W) {
-          const uint32_t x = p.v_win[(win_base + static_cast<int64_t>(pos - L) * p.Hkv) * D + d];
-          v[e >> 1] |= (e & 1) ? (x << 16) : x;
-        }
-      }
-      *reinterpret_cast<u32x4_t*>(dst) = v;
-    }
+    fix_boundary<D>(lds_k, lds_v, ts, t0, te, L, W, p.k_win, p.v_win, win_base, p.Hkv, tid, RG_THREADS);
     return true;
   };
 
