@@ -190,6 +190,60 @@ GSS_DEV void post_addnorm_row(const GemmParams& p, int row, int lane) {
   }
 }
 
+// Epilogue of output tile (f, n) of the workgroup whose first feature is f0, on its reduced sum s (lane: activation
+// row n*16 + l16, features f0 + f*16 + g4*4 .. +3). The GEMM output is rounded to bf16 first, as a bf16 torch linear
+// writes it.
+template <int EPI, bool POST>
+GSS_DEV void gemm_epilogue(const GemmParams& p, int f0, int f, int n, floatx4_t s, int l16, int g4) {
+  const int row = n * 16 + l16;            // activation row
+  const int feat = f0 + f * 16 + g4 * 4;   // first of this lane's 4 consecutive output features
+  float y0 = s[0], y1 = s[1], y2 = s[2], y3 = s[3];
+  if constexpr (EPI == EPI_PLAIN) {
+    if (p.out_f32) {
+      *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) = s;
+    } else if constexpr (POST) {  // the rows are handed to the workgroup that runs the norm
+      uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy +
+                                                  feat);
+      st_agent(dst, pack_bf16x2(y0, y1));
+      st_agent(dst + 1, pack_bf16x2(y2, y3));
+    } else {
+      *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) =
+          u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+    }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    // features (gate_i, up_i, gate_i+1, up_i+1), i = feat / 2
+    const float g0 = round_bf16(y0), u0 = round_bf16(y1), g1 = round_bf16(y2), u1 = round_bf16(y3);
+    const float s0 = round_bf16(g0 / (1.f + expf(-g0))), s1 = round_bf16(g1 / (1.f + expf(-g1)));
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat / 2) =
+        pack_bf16x2(u0 * s0, u1 * s1);
+  } else {  // EPI_ROPE
+    const int b = row / p.W, w = row % p.W;
+    const int head = feat / p.D, d = feat % p.D;  // 4 features never straddle a head (D % 16 == 0)
+    float o[4] = {round_bf16(y0), round_bf16(y1), round_bf16(y2), round_bf16(y3)};
+    if (head < p.Hq + p.Hkv) {
+      const int pos = p.seq_lens[b] + (p.pos_delta ? p.pos_delta[b] : 0) + w;
+#pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        if (d + e < p.rot_dim) {
+          const float fr = static_cast<float>(pos) * p.inv_freq[(d + e) >> 1];
+          const float c = round_bf16(cosf(fr)), sn = round_bf16(sinf(fr));
+          const float x0 = o[e], x1 = o[e + 1];
+          o[e] = round_bf16(round_bf16(x0 * c) - round_bf16(x1 * sn));
+          o[e + 1] = round_bf16(round_bf16(x1 * c) + round_bf16(x0 * sn));
+        }
+      }
+    }
+    uint16_t* dst;
+    if (head < p.Hq)
+      dst = p.q_out + (static_cast<int64_t>(row) * p.Hq + head) * p.D + d;
+    else if (head < p.Hq + p.Hkv)
+      dst = p.k_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq)) * p.D + d;
+    else
+      dst = p.v_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq - p.Hkv)) * p.D + d;
+    *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+  }
+}
+
 template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8, bool POST = false>
 __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw) {
   extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD]
@@ -281,56 +335,8 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
     for (int n = 0; n < NT; ++n) red[((wv * FT + f) * NT + n) * 64 + lane] = acc[f][n];
   __syncthreads();
 
-  // Epilogue of tile (f, n) on its reduced sum (wave v owns the tiles with (f * NT + n) % NW == v).
-  auto epilogue = [&](int f, int n, floatx4_t s) {
-    const int row = n * 16 + l16;            // activation row
-    const int feat = f0 + f * 16 + g4 * 4;   // first of this lane's 4 consecutive output features
-    float y0 = s[0], y1 = s[1], y2 = s[2], y3 = s[3];
-    if constexpr (EPI == EPI_PLAIN) {
-      if (p.out_f32) {
-        *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) = s;
-      } else if constexpr (POST) {  // the rows are handed to the workgroup that runs the norm
-        uint32_t* dst = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy +
-                                                    feat);
-        st_agent(dst, pack_bf16x2(y0, y1));
-        st_agent(dst + 1, pack_bf16x2(y2, y3));
-      } else {
-        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat) =
-            u32x2_t{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
-      }
-    } else if constexpr (EPI == EPI_SWIGLU) {
-      // features (gate_i, up_i, gate_i+1, up_i+1), i = feat / 2
-      const float g0 = round_bf16(y0), u0 = round_bf16(y1), g1 = round_bf16(y2), u1 = round_bf16(y3);
-      const float s0 = round_bf16(g0 / (1.f + expf(-g0))), s1 = round_bf16(g1 / (1.f + expf(-g1)));
-      *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat / 2) =
-          pack_bf16x2(u0 * s0, u1 * s1);
-    } else {  // EPI_ROPE
-      const int b = row / p.W, w = row % p.W;
-      const int head = feat / p.D, d = feat % p.D;  // 4 features never straddle a head (D % 16 == 0)
-      float o[4] = {round_bf16(y0), round_bf16(y1), round_bf16(y2), round_bf16(y3)};
-      if (head < p.Hq + p.Hkv) {
-        const int pos = p.seq_lens[b] + (p.pos_delta ? p.pos_delta[b] : 0) + w;
-#pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          if (d + e < p.rot_dim) {
-            const float fr = static_cast<float>(pos) * p.inv_freq[(d + e) >> 1];
-            const float c = round_bf16(cosf(fr)), sn = round_bf16(sinf(fr));
-            const float x0 = o[e], x1 = o[e + 1];
-            o[e] = round_bf16(round_bf16(x0 * c) - round_bf16(x1 * sn));
-            o[e + 1] = round_bf16(round_bf16(x1 * c) + round_bf16(x0 * sn));
-          }
-        }
-      }
-      uint16_t* dst;
-      if (head < p.Hq)
-        dst = p.q_out + (static_cast<int64_t>(row) * p.Hq + head) * p.D + d;
-      else if (head < p.Hq + p.Hkv)
-        dst = p.k_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq)) * p.D + d;
-      else
-        dst = p.v_out + (static_cast<int64_t>(row) * p.Hkv + (head - p.Hq - p.Hkv)) * p.D + d;
-      *reinterpret_cast<u32x2_t*>(dst) = u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-    }
-  };
+  // epilogue of tile (f, n) on its reduced sum (wave v owns the tiles with (f * NT + n) % NW == v)
+  auto epilogue = [&](int f, int n, floatx4_t s) { gemm_epilogue<EPI, POST>(p, f0, f, n, s, l16, g4); };
   auto reduced = [&](int f, int n) {
     floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
     for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
@@ -402,9 +408,117 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   }
 }
 
+// Persistent variant for shapes with many column tiles and one load pass per tile (every wave's k-steps fit one
+// unrolled pass): gridDim.x workgroups (about one per CU) walk the column tiles t = blockIdx.x, + gridDim.x, ...
+// The activations of a wave's k-steps are loaded once and reused for every tile; the next tile's weights are
+// loaded into the other register set before the current tile's MFMAs, reduction and epilogue, so a workgroup keeps
+// its weight stream in flight across tiles. The k partition over the waves and the wave-order reduction are those
+// of gemm_kernel, so both produce the same bits for the same shape and every row count.
+template <int FT, int NT, int UNR, int EPI>
+__global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, int ksw, int n_tiles) {
+  extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int ksteps = p.Kd / 32;
+  const int s_beg = wv * ksw, s_end = min(ksteps, s_beg + ksw);  // ksw <= UNR: one pass
+
+  // Every load below is unconditional (clamped indices), so the compiler can count the loads in flight and wait
+  // only for the older register set: activation rows past M read row 0 (their outputs are never stored), k-steps
+  // past the wave's range read its last k-step and are skipped at the MFMA.
+  u32x4_t xb[UNR][NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int r = n * 16 + l16;
+    const uint16_t* xr = p.x + static_cast<int64_t>(r < p.M ? r : 0) * p.ldx + g4 * 8;
+#pragma unroll
+    for (int u = 0; u < UNR; ++u)
+      xb[u][n] = *reinterpret_cast<const u32x4_t*>(xr + min(s_beg + u, ksteps - 1) * 32);
+  }
+  auto load_w = [&](int t, u32x4_t(&wa)[UNR][FT]) {
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+      const int row = min(t * FT * 16 + f * 16 + l16, p.N - 1);  // rows past N repeat the last (never stored)
+      const uint16_t* wr = p.w + static_cast<int64_t>(row) * p.ldw + g4 * 8;
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) wa[u][f] = *reinterpret_cast<const u32x4_t*>(wr + min(s_beg + u, ksteps - 1) * 32);
+    }
+  };
+  auto tile = [&](int t, const u32x4_t(&wa)[UNR][FT]) {
+    floatx4_t acc[FT][NT];
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < UNR; ++u) {
+      if (s_beg + u < s_end) {  // wave-uniform
+#pragma unroll
+        for (int f = 0; f < FT; ++f)
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+            acc[f][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa[u][f]),
+                                                                __builtin_bit_cast(bf16x8_t, xb[u][n]), acc[f][n], 0,
+                                                                0, 0);
+      }
+    }
+    __syncthreads();  // the previous tile's partials have been read
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) red[((wv * FT + f) * NT + n) * 64 + lane] = acc[f][n];
+    __syncthreads();
+    const int f0 = t * FT * 16;
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        if ((f * NT + n) % NW != wv || n * 16 + l16 >= p.M || f0 + f * 16 + g4 * 4 >= p.N) continue;
+        floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
+        for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
+        gemm_epilogue<EPI, false>(p, f0, f, n, s, l16, g4);
+      }
+  };
+  // two register sets, alternating: while one tile is computed, the next one's weights stream into the other set.
+  // The steady state (two tiles per iteration) always has a next tile, so its loads are issued unconditionally.
+  const int G = gridDim.x;
+  const int n_my = (n_tiles - static_cast<int>(blockIdx.x) + G - 1) / G;  // tiles of this workgroup (>= 1)
+  auto tile_at = [&](int i) { return static_cast<int>(blockIdx.x) + i * G; };
+  u32x4_t wa[UNR][FT], wb[UNR][FT];
+  load_w(tile_at(0), wa);
+  int i = 0;
+  for (; i + 2 < n_my; i += 2) {
+    load_w(tile_at(i + 1), wb);
+    tile(tile_at(i), wa);
+    load_w(tile_at(i + 2), wa);
+    tile(tile_at(i + 1), wb);
+  }
+  if (i + 1 < n_my) {
+    load_w(tile_at(i + 1), wb);
+    tile(tile_at(i), wa);
+    tile(tile_at(i + 1), wb);
+  } else {
+    tile(tile_at(i), wa);
+  }
+}
+
 // Launch shape knobs (process-wide): the most waves per workgroup, the features per workgroup (0 = automatic) and
 // the most k splits over workgroups (1 = none).
 int g_max_nw = MAX_NW, g_ft = 0, g_max_ksplit = 2;
+int g_stream_wgs = 0;  // workgroups of the persistent GEMM (0: the device's CU count)
+
+// workgroups of the persistent kernel: one per CU of the current device (queried once)
+int stream_wgs() {
+  if (g_stream_wgs > 0) return g_stream_wgs;
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  return cus;
+}
 
 // Workspace: per-column-tile counters and the post-norm counter at a fixed offset (so calls of every shape share one
 // workspace), then the split-K partials.
@@ -461,6 +575,15 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
     }
     return gss_launch_status();
   } else {
+    if constexpr (!POST) {
+      // more column tiles than CUs and one load pass per tile (a function of N and Kd only, so every row count
+      // takes the same kernel): the persistent kernel, one workgroup per CU walking the tiles
+      const int G = stream_wgs();
+      if (p.ksplit == 1 && ksw <= 4 && n_tiles > G) {
+        hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI>), dim3(G), block, lds, st, p, ksw, n_tiles);
+        return gss_launch_status();
+      }
+    }
     if constexpr (FT + NT <= 3) {
       if (ksw % 8 == 0) {
         hipLaunchKernelGGL((gemm_kernel<FT, NT, 8, EPI, PRO_NONE, 8, POST>), grid, block, lds, st, p, ksw);
