@@ -389,8 +389,8 @@ def main():
                      "algorithmic_bytes": ab, "avg_us": round(d_us, 2), "L": L, "W": Kw,
                      "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "verify_avg_us": round(v_us, 2)},
-        "roofline_batched": {"bound": "hbm", "kernel": "gss_draft_attn, 32 sequences, prefixes U[1024, 12288] "
-                                                       "(seed 3), W=17, one paged pool",
+        "roofline_batched": {"bound": "hbm", "kernel": "gss_draft_attn (wide kernel), 32 sequences, prefixes "
+                                                       "U[1024, 12288] (seed 3), W=17, one paged pool",
                              "achieved": round(b_bytes / (b_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(b_bytes / (b_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes": b_bytes, "avg_us": round(b_us, 2)},
