@@ -184,8 +184,9 @@ GSS_DEV int valid_splits(int L, int W, int tps) {
   return (n_tiles + tps - 1) / tps;
 }
 
-template <int D, int NGW>
-__global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams p) {
+template <int D, int NGW, int RWT>
+__global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p) {
+  constexpr int NW = KL * RWT;  // waves per workgroup
   constexpr int KS = D / 32;   // MFMA K-steps over the head dim
   constexpr int DT = D / 16;   // 16-row tiles of the head dim (O^T M-tiles)
   constexpr int CH = D / 8;    // 16-byte chunks per K row
@@ -204,7 +205,7 @@ __global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams
   const int u = blockIdx.x / (8 * p.RG) * 8 + r8 % 8, rg = r8 / 8;
   if (u >= p.n_units) return;  // padding of the last group of 8 units
   const int s = u % p.n_split, kvh = (u / p.n_split) % p.Hkv, b = u / (p.n_split * p.Hkv);
-  const int tid = threadIdx.x, lane = tid & 63, NW = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kl = wv % KL, rw = wv / KL;                       // key lane, row wave
   const int l16 = lane & 15, g4 = lane >> 4;
@@ -223,6 +224,7 @@ __global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams
   // are never written; N-tiles g >= ng are skipped (never computed).
   const int tb_base = p.TPG / p.RW, tb_extra = p.TPG % p.RW;
   const int ng = tb_base + (rw < tb_extra ? 1 : 0);
+  __builtin_assume(ng >= NGW - 1 && ng <= NGW);  // the host deals NGW or NGW - 1 tiles to every row wave
   const int nt0 = rg * p.TPG + rw * tb_base + min(rw, tb_extra);
   bf16x8_t qf[NGW][KS];
 #pragma unroll
@@ -268,7 +270,10 @@ __global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams
     const int pgv = lane < KL * (TILE / PAGE) && st * KL * (TILE / PAGE) + lane < (t_end - t_beg) * (TILE / PAGE)
                         ? spages[st * KL * (TILE / PAGE) + lane]
                         : 0;
-    for (int ii = wv; ii < STAGE_INSTR; ii += NW) {
+#pragma unroll 1  // unrolled, the per-instruction lane offsets are hoisted out of the stage loop and spilled
+    for (int i = 0; i < (STAGE_INSTR + NW - 1) / NW; ++i) {
+      const int ii = wv + i * NW;
+      if (ii >= STAGE_INSTR) break;
       const bool is_v = ii >= KL * TILE_INSTR;
       const int iv = is_v ? ii - KL * TILE_INSTR : ii;
       const int tl = iv / TILE_INSTR, ib = iv % TILE_INSTR;
@@ -277,22 +282,23 @@ __global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams
       const int pblk = ib / PAGE_INSTR, pat = ib % PAGE_INSTR;
       const int pos0 = t * TILE + pblk * PAGE;  // first position of the page
       const int kr = pat * 64 + lane;
-      int off;
-      bool in_prefix;
+      int off, first;  // element offset in the (page, head) block; position of the chunk's first token
       if (is_v) {
         const int vd = kr >> 1, vh = (kr & 1) ^ ((vd >> 3) & 1);
         off = vd * PAGE + vh * 8;
-        in_prefix = pos0 + vh * 8 < L;
+        first = pos0 + vh * 8;
       } else {
         const int ktok = kr / CH;
         off = ktok * D + ((kr % CH) ^ (ktok & (CH - 1))) * 8;
-        in_prefix = pos0 + ktok < L;
+        first = pos0 + ktok;
       }
       const int64_t page = __builtin_amdgcn_readlane(pgv, tl * (TILE / PAGE) + pblk);
       const uint16_t* base = (is_v ? p.v_pages : p.k_pages) + (page * p.Hkv + kvh) * head_stride;
-      if (in_prefix)
-        __builtin_amdgcn_global_load_lds((gvoid_t*)(base + off),
-                                         (lvoid_t*)(buf + (is_v ? KL * TILE_EL : 0) + iv * 512), 16, 0, 0);
+      lvoid_t* dst = (lvoid_t*)(buf + (is_v ? KL * TILE_EL : 0) + iv * 512);
+      if (pos0 + PAGE <= L)  // page wholly inside the prefix (wave-uniform): no per-lane test
+        __builtin_amdgcn_global_load_lds((gvoid_t*)(base + off), dst, 16, 0, 0);
+      else if (first < L)
+        __builtin_amdgcn_global_load_lds((gvoid_t*)(base + off), dst, 16, 0, 0);
     }
   };
   // Tiles that reach past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
@@ -311,9 +317,9 @@ __global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams
   // each whole (4 m-tiles of 16 keys), for its ng N-tiles. Scores come out of the MFMA in the log2 domain (the
   // queries are pre-scaled). Each row keeps a reference max m that trails its running max by at most RESCALE_SLACK,
   // and P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more than the slack
-  // (rare after the first tiles) does the wave move the references and rescale O and l. Row maxima: 16 values per
-  // lane, then two xor-shuffles over the lanes of a row. P^T is packed to bf16 in the lane that scored it, and
-  // O^T += V^T P^T over 2 K-steps of 32 keys.
+  // (rare after the first tiles) does the wave take the row maxima (two xor-shuffles over the row's lanes), move the
+  // references and rescale O and l. P^T is packed to bf16 in the lane that scored it, and O^T += V^T P^T over
+  // 2 K-steps of 32 keys.
   floatx4_t o[NGW][DT];
   float m_run[NGW], l_run[NGW];
 #pragma unroll
@@ -337,95 +343,99 @@ __global__ void __launch_bounds__(64 * KL * RW_MAX) attn_split_kernel(AttnParams
     if (tb >= t_end * TILE) continue;  // wave-uniform: this key lane has no tile in the last stage
     const uint16_t* tk = smem + (st & 1) * Lds<D>::STAGE_EL + kl * TILE_EL;
     const uint16_t* tv = tk + KL * TILE_EL;
-    floatx4_t sacc[NGW][4];
+    // the tile in two halves of 32 keys (half hh: m-tiles 2hh and 2hh+1, the P^T slots 0..3 and 4..7 of K-step hh),
+    // each: scores, mask, row maxima and reference moves, P^T, then O^T += V^T P^T. LDS fragments are read one step
+    // ahead of the MFMAs that use them.
 #pragma unroll
-    for (int g = 0; g < NGW; ++g)
+    for (int hh = 0; hh < 2; ++hh) {
+      floatx4_t sacc[NGW][2];
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) sacc[g][mt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      for (int g = 0; g < NGW; ++g) sacc[g][0] = sacc[g][1] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      // K-step outer, m-tile inner: consecutive MFMAs go to 2 * ng different accumulators, so a dependent one
+      // (same accumulator, next K-step) is never issued right behind its predecessor
+      auto kfrag = [&](int i) {  // i = ks * 2 + mt over the half's 2 m-tiles
+        return *reinterpret_cast<const bf16x8_t*>(&tk[k_lds_index<D>((2 * hh + (i & 1)) * 16 + l16, (i >> 1) * 4 + g4)]);
+      };
+      bf16x8_t a_cur = kfrag(0);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {  // one K fragment live at a time; it feeds the ng N-tiles
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&tk[k_lds_index<D>(mt * 16 + l16, ks * 4 + g4)]);
+      for (int i = 0; i < 2 * KS; ++i) {
+        bf16x8_t a_nxt = a_cur;
+        if (i + 1 < 2 * KS) a_nxt = kfrag(i + 1);
 #pragma unroll
         for (int g = 0; g < NGW; ++g)
-          if (g < ng) sacc[g][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[g][ks], sacc[g][mt], 0, 0, 0);
+          if (g < ng)
+            sacc[g][i & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, qf[g][i >> 1], sacc[g][i & 1], 0, 0, 0);
+        a_cur = a_nxt;
       }
-    }
-    if (tb + TILE > L) {  // keys past the prefix: the window mask (wave-uniform branch)
+      if (tb + TILE > L) {  // keys past the prefix: the window mask (wave-uniform branch)
 #pragma unroll
-      for (int g = 0; g < NGW; ++g) {
-        const int n = (nt0 + g) * 16 + l16;
-        const int roww = (n < p.R ? n : 0) / p.G;  // the row's window index
+        for (int g = 0; g < NGW; ++g) {
+          const int n = (nt0 + g) * 16 + l16;
+          const int roww = (n < p.R ? n : 0) / p.G;  // the row's window index
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+          for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int pos = tb + mt * 16 + g4 * 4 + i;
-            const int wj = pos - L;
-            const bool vis = pos < L || (wj < W && (roww >= nc || wj <= roww));
-            if (!vis) sacc[g][mt][i] = -INFINITY;
-          }
+            for (int i = 0; i < 4; ++i) {
+              const int pos = tb + (2 * hh + mt) * 16 + g4 * 4 + i;
+              const int wj = pos - L;
+              const bool vis = pos < L || (wj < W && (roww >= nc || wj <= roww));
+              if (!vis) sacc[g][mt][i] = -INFINITY;
+            }
+        }
       }
-    }
-    // row maxima and reference moves of every N-tile, then per K-step kk (keys of m-tiles 2kk in P^T slots 0..3,
-    // 2kk+1 in slots 4..7): the P^T operands of all N-tiles, then each V^T fragment read once for all of them
-    float m_use[NGW], ls[NGW];
-#pragma unroll
-    for (int g = 0; g < NGW; ++g) {
-      m_use[g] = 0.f;
-      ls[g] = 0.f;
-      if (g >= ng) continue;  // wave-uniform
-      float mx = -INFINITY;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-        mx = fmaxf(mx, fmaxf(fmaxf(sacc[g][mt][0], sacc[g][mt][1]), fmaxf(sacc[g][mt][2], sacc[g][mt][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // the row's reference moves only when its max exceeds it by more than the slack (or on its first visible
-      // tile, m_run = -inf); a tile whose keys are all masked (mx = -inf) never moves it
-      if (__any(mx > m_run[g] + RESCALE_SLACK)) {  // wave-uniform: rescale O and l of the rows that moved
-        const float m_new = mx > m_run[g] + RESCALE_SLACK ? mx : m_run[g];
-        // 1 for rows that keep their reference (also -inf: no visible key yet, where -inf - -inf would be NaN),
-        // 0 on a row's first visible tile
-        const float alpha = m_new == m_run[g] ? 1.f : fast_exp2(m_run[g] - m_new);
-        m_run[g] = m_new;
-        l_run[g] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * alpha;
-      }
-      m_use[g] = m_run[g] == -INFINITY ? 0.f : m_run[g];  // a row with no visible key yet: P = 0
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
       bf16x8_t pb[NGW];
 #pragma unroll
       for (int g = 0; g < NGW; ++g) {
-        if (g >= ng) continue;
+        if (g >= ng) continue;  // wave-uniform
+        // the lane's own max over its 8 scores of the row; a row's reference moves only when its max exceeds it by
+        // more than the slack (or on its first visible keys, m_run = -inf), so the row max over the row's 4 lanes
+        // (two xor-shuffles) is needed only when some lane's own max does: the wave votes first. Keys that are all
+        // masked (mx = -inf) never move a reference.
+        float mx = fmaxf(fmaxf(fmaxf(sacc[g][0][0], sacc[g][0][1]), fmaxf(sacc[g][0][2], sacc[g][0][3])),
+                         fmaxf(fmaxf(sacc[g][1][0], sacc[g][1][1]), fmaxf(sacc[g][1][2], sacc[g][1][3])));
+        if (__any(mx > m_run[g] + RESCALE_SLACK)) {  // wave-uniform: rescale O and l of the rows that moved
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          const float m_new = mx > m_run[g] + RESCALE_SLACK ? mx : m_run[g];
+          // 1 for rows that keep their reference (also -inf: no visible key yet, where -inf - -inf would be NaN),
+          // 0 on a row's first visible keys
+          const float alpha = m_new == m_run[g] ? 1.f : fast_exp2(m_run[g] - m_new);
+          m_run[g] = m_new;
+          l_run[g] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * alpha;
+        }
+        const float m_use = m_run[g] == -INFINITY ? 0.f : m_run[g];  // a row with no visible key yet: P = 0
         uint32_t pk[4];
+        float ls = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const floatx4_t& sv = sacc[g][2 * kk + (j >> 1)];
-          const float p0 = fast_exp2(sv[(2 * j) & 3] - m_use[g]);
-          const float p1 = fast_exp2(sv[(2 * j + 1) & 3] - m_use[g]);
-          ls[g] += p0 + p1;
+          const floatx4_t& sv = sacc[g][j >> 1];
+          const float p0 = fast_exp2(sv[(2 * j) & 3] - m_use);
+          const float p1 = fast_exp2(sv[(2 * j + 1) & 3] - m_use);
+          ls += p0 + p1;
           pk[j] = cvt_pk_bf16(p0, p1);
         }
+        l_run[g] += ls;
         pb[g] = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
       }
+      auto vfrag = [&](int dt) {
+        const int d = dt * 16 + l16;
+        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh) * D + d) * PAGE + vrd]);
+        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh + 1) * D + d) * PAGE + vrd]);
+        return __builtin_bit_cast(bf16x8_t, u32x4_t{v0[0], v0[1], v1[0], v1[1]});
+      };
+      bf16x8_t v_cur = vfrag(0);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int d = dt * 16 + l16;
-        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * kk) * D + d) * PAGE + vrd]);
-        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * kk + 1) * D + d) * PAGE + vrd]);
-        const bf16x8_t va = __builtin_bit_cast(bf16x8_t, u32x4_t{v0[0], v0[1], v1[0], v1[1]});
+        bf16x8_t v_nxt = v_cur;
+        if (dt + 1 < DT) v_nxt = vfrag(dt + 1);
 #pragma unroll
         for (int g = 0; g < NGW; ++g)
-          if (g < ng) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[g], o[g][dt], 0, 0, 0);
+          if (g < ng) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_cur, pb[g], o[g][dt], 0, 0, 0);
+        v_cur = v_nxt;
       }
     }
-#pragma unroll
-    for (int g = 0; g < NGW; ++g) l_run[g] += ls[g];
   }
 
   // ---- combine the KL key lanes of each row wave in lane order (fp32, through LDS), normalize, write.
@@ -871,8 +881,11 @@ template <int D>
 int set_lds_limits() {
   static bool done = false;  // allow the dynamic LDS beyond the default 64 KB (set once, before use)
   if (!done) {
-    const void* wide[] = {reinterpret_cast<const void*>(&attn_split_kernel<D, 2>),
-                          reinterpret_cast<const void*>(&attn_split_kernel<D, 3>)};
+    const void* wide[] = {reinterpret_cast<const void*>(&attn_split_kernel<D, 2, 1>),
+                          reinterpret_cast<const void*>(&attn_split_kernel<D, 2, 2>),
+                          reinterpret_cast<const void*>(&attn_split_kernel<D, 2, 3>),
+                          reinterpret_cast<const void*>(&attn_split_kernel<D, 2, 4>),
+                          reinterpret_cast<const void*>(&attn_split_kernel<D, 3, 4>)};
     for (const void* f : wide)
       if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, Lds<D>::TOTAL) != hipSuccess)
         return GSS_ERR_LAUNCH;
@@ -895,11 +908,18 @@ int launch_d(const AttnParams& p, int bs, bool wide, int ng, hipStream_t st) {
   if (wide) {
     const dim3 block(64 * KL * p.RW);
     constexpr size_t lds = Lds<D>::TOTAL;
-    // one N-tile per wave runs on the two-tile instantiation (only its first tile is computed)
-    if (ng <= 2)
-      hipLaunchKernelGGL((attn_split_kernel<D, 2>), grid, block, lds, st, p);
+    // row waves x N-tiles per row wave: 1..4 x <= 2 (one N-tile per wave runs on the two-tile instantiation, only
+    // its first tile computed), or 4 x 3
+    if (ng > 2)
+      hipLaunchKernelGGL((attn_split_kernel<D, 3, 4>), grid, block, lds, st, p);
+    else if (p.RW == 4)
+      hipLaunchKernelGGL((attn_split_kernel<D, 2, 4>), grid, block, lds, st, p);
+    else if (p.RW == 3)
+      hipLaunchKernelGGL((attn_split_kernel<D, 2, 3>), grid, block, lds, st, p);
+    else if (p.RW == 2)
+      hipLaunchKernelGGL((attn_split_kernel<D, 2, 2>), grid, block, lds, st, p);
     else
-      hipLaunchKernelGGL((attn_split_kernel<D, 3>), grid, block, lds, st, p);
+      hipLaunchKernelGGL((attn_split_kernel<D, 2, 1>), grid, block, lds, st, p);
   } else {
     constexpr size_t lds = LdsRG<D>::TOTAL;
     if (ng == 1)
