@@ -413,10 +413,12 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
 // The activations of a wave's k-steps are loaded once and reused for every tile; the next tile's weights are
 // loaded into the other register set before the current tile's MFMAs, reduction and epilogue, so a workgroup keeps
 // its weight stream in flight across tiles. The k partition over the waves and the wave-order reduction are those
-// of gemm_kernel, so both produce the same bits for the same shape and every row count.
-template <int FT, int NT, int UNR, int EPI>
+// of gemm_kernel, so both produce the same bits for the same shape and every row count. With PRO_ADDNORM the
+// workgroup first issues its first tile's weight loads, then builds the normalized activation rows in LDS (the
+// arithmetic of gss_add_rmsnorm, as in gemm_kernel's prologue) while they are in flight.
+template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8>
 __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, int ksw, int n_tiles) {
-  extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials
+  extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD]
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int ksteps = p.Kd / 32;
@@ -425,15 +427,7 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
   // Every load below is unconditional (clamped indices), so the compiler can count the loads in flight and wait
   // only for the older register set: activation rows past M read row 0 (their outputs are never stored), k-steps
   // past the wave's range read its last k-step and are skipped at the MFMA.
-  u32x4_t xb[UNR][NT];
-#pragma unroll
-  for (int n = 0; n < NT; ++n) {
-    const int r = n * 16 + l16;
-    const uint16_t* xr = p.x + static_cast<int64_t>(r < p.M ? r : 0) * p.ldx + g4 * 8;
-#pragma unroll
-    for (int u = 0; u < UNR; ++u)
-      xb[u][n] = *reinterpret_cast<const u32x4_t*>(xr + min(s_beg + u, ksteps - 1) * 32);
-  }
+  u32x4_t xb[UNR][NT];  // this wave's activation fragments, filled once below (after the first weight loads)
   auto load_w = [&](int t, u32x4_t(&wa)[UNR][FT]) {
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
@@ -485,6 +479,29 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
   auto tile_at = [&](int i) { return static_cast<int>(blockIdx.x) + i * G; };
   u32x4_t wa[UNR][FT], wb[UNR][FT];
   load_w(tile_at(0), wa);
+  if constexpr (PRO == PRO_ADDNORM) {
+    // the normalized rows, one wavefront per row, into LDS; workgroup 0 also stores the updated residual
+    uint16_t* xs = reinterpret_cast<uint16_t*>(red + NW * FT * NT * 64);
+    for (int r = wv; r < p.M; r += NW) addnorm_row<E>(p, r, lane, xs, blockIdx.x == 0 && p.h_out != nullptr);
+    __syncthreads();
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int r = n * 16 + l16;
+#pragma unroll
+      for (int u = 0; u < UNR; ++u)
+        xb[u][n] = *reinterpret_cast<const u32x4_t*>(xs + (r < p.M ? r : 0) * (p.Kd + XPAD) +
+                                                     min(s_beg + u, ksteps - 1) * 32 + g4 * 8);
+    }
+  } else {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int r = n * 16 + l16;
+      const uint16_t* xr = p.x + static_cast<int64_t>(r < p.M ? r : 0) * p.ldx + g4 * 8;
+#pragma unroll
+      for (int u = 0; u < UNR; ++u)
+        xb[u][n] = *reinterpret_cast<const u32x4_t*>(xr + min(s_beg + u, ksteps - 1) * 32);
+    }
+  }
   int i = 0;
   for (; i + 2 < n_my; i += 2) {
     load_w(tile_at(i + 1), wb);
@@ -566,6 +583,17 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
     lds += static_cast<size_t>(p.M) * (p.Kd + XPAD) * sizeof(uint16_t);
     if (ksw > 4) return GSS_ERR_UNSUPPORTED;  // one pass of 4 k-steps per wave: Kd <= 32 * 4 * MAX_NW
     if (lds > MAX_LDS) return GSS_ERR_UNSUPPORTED;
+    const int G = stream_wgs();
+    if (p.ksplit == 1 && n_tiles > G) {  // the persistent kernel (same rule as without the prologue)
+      switch (p.Kd / 64) {
+        case 4: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 4>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
+        case 8: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 8>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
+        case 16: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 16>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
+        case 24: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 24>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
+        default: return GSS_ERR_UNSUPPORTED;
+      }
+      return gss_launch_status();
+    }
     switch (p.Kd / 64) {
       case 4: hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO, 4>), grid, block, lds, st, p, ksw); break;
       case 8: hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO, 8>), grid, block, lds, st, p, ksw); break;

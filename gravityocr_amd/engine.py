@@ -60,6 +60,11 @@ class GssEngine:
         self.fuse_norm_rows = 0
         # sandwich norms in the o_proj / down GEMM epilogues (one launch less each) instead of gss_add_rmsnorm
         self.post_norm = False
+        # the post-attention norms in the gate_up GEMM's prologue (persistent kernel: once per CU, while the first
+        # weight tiles load) instead of a gss_add_rmsnorm launch; bit-identical to the separate norm. Used where it
+        # pays: at most 12 rows (one row per wave of the GEMM's 12; the 1-row AR step gains ~21 us per forward, a
+        # 17-row round forward loses ~25 us) and a hidden size the prologue supports (a multiple of 512, <= 1536)
+        self.fuse_gate_norm = True
         self.device = torch.device(device)
         self.max_bs, self.max_len, self.max_win = max_bs, max_len, max_win
         dev, bf = self.device, torch.bfloat16
@@ -156,10 +161,12 @@ class GssEngine:
     def _forward_own(self, b: _Bufs, n_causal, sl, pt, pos_delta, mkl) -> torch.Tensor:
         """Decode forward on the batch-invariant GEMMs (b.x already holds the first input norm). Per layer:
         [qkv + RoPE + staging], attention (+ split merge), o_proj, residual norm, [gate_up + SwiGLU], down,
-        residual norm (the norms inside the o_proj / down GEMM epilogues when post_norm is set)."""
+        residual norm (the norms inside the o_proj / down GEMM epilogues when post_norm is set; the post-attention
+        norms inside the gate_up prologue when fuse_gate_norm is set)."""
         c = self.cfg
         bs, W = b.bs, b.W
         ws = self.ws_gemm
+        h, h_alt = b.h, b.h2  # the residual stream; the gate_up prologue writes the updated one to the other buffer
         for l in range(c.n_layers):
             K.gemm_rope_stage(b.x, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], rot_dim=c.rot_dim,
                               pos_delta=pos_delta, workspace=ws)
@@ -168,16 +175,22 @@ class GssEngine:
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
             if self.post_norm:
                 K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a, workspace=ws,
-                       post=dict(h=b.h, w_post=self.n_psa[l], w_next=self.n_pa[l], x=b.x, eps=c.rms_eps))
+                       post=dict(h=h, w_post=self.n_psa[l], w_next=self.n_pa[l], x=b.x, eps=c.rms_eps))
                 K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
                 K.gemm(b.act, self.wdown[l], b.a, workspace=ws,
-                       post=dict(h=b.h, w_post=self.n_pm[l], w_next=nxt, x=b.x, eps=c.rms_eps))
+                       post=dict(h=h, w_post=self.n_pm[l], w_next=nxt, x=b.x, eps=c.rms_eps))
             else:
                 K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a, workspace=ws)
-                K.add_rmsnorm(b.a, self.n_psa[l], b.h, self.n_pa[l], b.x, c.rms_eps)
-                K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
+                if self.fuse_gate_norm and bs * W <= 12 and c.hidden % 512 == 0 and c.hidden <= 1536:
+                    K.gemm_swiglu(None, self.wgu[l], b.act, workspace=ws,
+                                  pro=dict(a=b.a, h_in=h, h_out=h_alt, w_post=self.n_psa[l], w_next=self.n_pa[l],
+                                           eps=c.rms_eps))
+                    h, h_alt = h_alt, h
+                else:
+                    K.add_rmsnorm(b.a, self.n_psa[l], h, self.n_pa[l], b.x, c.rms_eps)
+                    K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
                 K.gemm(b.act, self.wdown[l], b.a, workspace=ws)
-                K.add_rmsnorm(b.a, self.n_pm[l], b.h, nxt, b.x, c.rms_eps)
+                K.add_rmsnorm(b.a, self.n_pm[l], h, nxt, b.x, c.rms_eps)
         K.gemm(b.x, self.lm_head, b.logits, workspace=ws)
         return b.logits.view(bs, W, c.vocab)
 

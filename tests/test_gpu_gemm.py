@@ -132,6 +132,12 @@ def test_norm_prologue_equals_unfused(cuda, M):
     gemm_swiglu(None, wgu, act, pro=dict(h_in=h, w_next=wn, eps=eps))
     torch.cuda.synchronize()
     assert torch.equal(act, act_ref)
+    # the engine's fused post-attention norm: residual input a, updated residual to h_out (the persistent GEMM)
+    gemm_swiglu(x, wgu, act_ref)
+    h_out2 = torch.empty_like(h)
+    gemm_swiglu(None, wgu, act, pro=dict(a=a, h_in=h, h_out=h_out2, w_post=wp, w_next=wn, eps=eps))
+    torch.cuda.synchronize()
+    assert torch.equal(act, act_ref) and torch.equal(h_out2, h_ref)
 
 
 @pytest.fixture(params=[1, 8], ids=["unsplit", "ksplit"])
