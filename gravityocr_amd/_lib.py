@@ -28,6 +28,7 @@ SIGNATURES = {
     "gss_kv_commit": ([_p, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
     "gss_ss_commit": ([_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _p], _i),
     "gss_kv_meta": ([_p, _i64, _i64, _p, _p, _i, _p, _p, _i64, _i, _p], _i),
+    "gss_log_append": ([_p, _i, _p, _p, _i, _p, _p, _i, _p, _p, _i, _p], _i),
     "gss_gemm_set_policy": ([_i, _i, _i], _i),
     "gss_gemm_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p, _p, _sz, _p], _i),
@@ -37,6 +38,7 @@ SIGNATURES = {
     "gss_rope_stage": ([_p, _i64, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _p], _i),
     "gss_rope_stage_mrope": ([_p, _i64, _p, _i, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _p], _i),
     "gss_rmsnorm": ([_p, _p, _p, _i, _i, _f, _p], _i),
+    "gss_embed_rmsnorm": ([_p, _p, _i, _p, _p, _p, _i, _i, _f, _p], _i),
     "gss_add_rmsnorm": ([_p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
     "gss_silu_mul": ([_p, _i64, _p, _i, _i, _p], _i),
 }

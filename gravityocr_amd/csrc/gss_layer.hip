@@ -108,6 +108,36 @@ __global__ void __launch_bounds__(64 * NORM_ROWS_PER_BLOCK) rmsnorm_kernel(const
   store_row<E>(out + static_cast<int64_t>(row) * H + lane * E, xv);
 }
 
+// Embedding lookup + the first input norm: h = table[ids[row]] (the residual stream), x = rmsnorm(h) * w. An id
+// outside [0, V) reads nothing and gives a zero row.
+template <int E>
+__global__ void __launch_bounds__(64 * NORM_ROWS_PER_BLOCK) embed_rmsnorm_kernel(const uint16_t* table,
+                                                                                 const int32_t* ids, int V,
+                                                                                 const uint16_t* w, uint16_t* h,
+                                                                                 uint16_t* x, int rows, float eps) {
+  constexpr int H = 64 * E;
+  const int row = blockIdx.x * NORM_ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int id = ids[row];
+  float xv[E], wv[E];
+  if (id >= 0 && id < V) {
+    load_row<E>(table + static_cast<int64_t>(id) * H + lane * E, xv);
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) xv[e] = 0.f;
+  }
+  load_row<E>(w + lane * E, wv);
+  const int64_t off = static_cast<int64_t>(row) * H + lane * E;
+  store_row<E>(h + off, xv);
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) ss += xv[e] * xv[e];
+  const float r = 1.f / sqrtf(wave_sum(ss) / static_cast<float>(H) + eps);
+#pragma unroll
+  for (int e = 0; e < E; ++e) xv[e] = wv[e] * round_bf16(xv[e] * r);
+  store_row<E>(x + off, xv);
+}
+
 // h = h + rmsnorm(a) * w_post ; x = rmsnorm(h) * w_next (sandwich-norm residual, then the next norm)
 template <int E>
 __global__ void __launch_bounds__(64 * NORM_ROWS_PER_BLOCK) add_rmsnorm_kernel(const uint16_t* a,
@@ -195,6 +225,24 @@ extern "C" int gss_rmsnorm(const void* x, const void* w, void* out, int rows, in
   switch (H / 64) {
 #define X(E) \
   case E: hipLaunchKernelGGL(rmsnorm_kernel<E>, grid, block, 0, st, xs, ws, os, rows, eps); break;
+    GSS_NORM_CASES(X)
+#undef X
+    default: return GSS_ERR_UNSUPPORTED;
+  }
+  return gss_launch_status();
+}
+
+extern "C" int gss_embed_rmsnorm(const void* table, const int32_t* ids, int V, const void* w, void* h, void* x,
+                                 int rows, int H, float eps, gss_stream_t stream) {
+  if (!table || !ids || !w || !h || !x || rows <= 0 || H <= 0 || V <= 0) return GSS_ERR_ARG;
+  if (H % 64 != 0 || H / 64 > MAX_E) return GSS_ERR_UNSUPPORTED;
+  const dim3 grid((rows + NORM_ROWS_PER_BLOCK - 1) / NORM_ROWS_PER_BLOCK), block(64 * NORM_ROWS_PER_BLOCK);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint16_t *ts = static_cast<const uint16_t*>(table), *ws = static_cast<const uint16_t*>(w);
+  uint16_t *hs = static_cast<uint16_t*>(h), *xs = static_cast<uint16_t*>(x);
+  switch (H / 64) {
+#define X(E) \
+  case E: hipLaunchKernelGGL(embed_rmsnorm_kernel<E>, grid, block, 0, st, ts, ids, V, ws, hs, xs, rows, eps); break;
     GSS_NORM_CASES(X)
 #undef X
     default: return GSS_ERR_UNSUPPORTED;

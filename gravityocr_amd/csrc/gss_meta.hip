@@ -91,6 +91,30 @@ __global__ void __launch_bounds__(256) kv_meta_kernel(MetaParams p) {
   for (int64_t k = t; k < n && start + k < p.cap; k += blockDim.x) p.kv_indices[start + k] = src[k];
 }
 
+// Round history on the device: row min(*ctr, capacity - 1) of up to three logs receives the current contents of
+// their source rows, then *ctr advances by one. One workgroup; every thread reads the counter before the barrier
+// that precedes its update.
+struct LogParams {
+  int64_t* ctr;
+  int capacity;
+  const int32_t* src[3];
+  int32_t* log[3];
+  int len[3];
+};
+
+__global__ void __launch_bounds__(256) log_append_kernel(LogParams p) {
+  const int64_t c = *p.ctr;
+  const int64_t li = c < 0 ? 0 : (c < p.capacity ? c : p.capacity - 1);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+    if (p.src[s] == nullptr) continue;
+    int32_t* dst = p.log[s] + li * p.len[s];
+    for (int i = threadIdx.x; i < p.len[s]; i += blockDim.x) dst[i] = p.src[s][i];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *p.ctr = c + 1;
+}
+
 }  // namespace
 
 extern "C" int gss_ss_commit(const int32_t* predict, const int32_t* accept_len, const int64_t* a0, int64_t a0_stride,
@@ -116,5 +140,18 @@ extern "C" int gss_kv_meta(const int32_t* req_to_token, int64_t r2t_stride, int6
   MetaParams p{req_to_token, r2t_stride, req_pool_indices, seq_lens, extra, kv_indptr, kv_indices, n_req,
                kv_indices_cap};
   hipLaunchKernelGGL(kv_meta_kernel, dim3(bs), dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  return gss_launch_status();
+}
+
+extern "C" int gss_log_append(int64_t* ctr, int capacity, const int32_t* src0, int32_t* log0, int len0,
+                              const int32_t* src1, int32_t* log1, int len1, const int32_t* src2, int32_t* log2,
+                              int len2, gss_stream_t stream) {
+  if (!ctr || capacity <= 0) return GSS_ERR_ARG;
+  LogParams p{ctr, capacity, {src0, src1, src2}, {log0, log1, log2}, {len0, len1, len2}};
+  for (int s = 0; s < 3; ++s) {
+    if (p.src[s] == nullptr) continue;
+    if (p.log[s] == nullptr || p.len[s] <= 0) return GSS_ERR_ARG;
+  }
+  hipLaunchKernelGGL(log_append_kernel, dim3(1), dim3(256), 0, static_cast<hipStream_t>(stream), p);
   return gss_launch_status();
 }

@@ -131,15 +131,19 @@ class GssEngine:
         sl = self.seq_lens[:bs] if seq_lens is None else seq_lens
         pt = self.page_table[:bs] if page_table is None else page_table
         mkl = self.max_len if max_kv_len is None else max_kv_len
-        if emb is not None:
-            b.h.copy_(emb.view(bs * W, c.hidden))
-        else:
-            torch.index_select(self.embed, 0, ids.reshape(-1), out=b.h)
         own = self.gemm_impl == "gss" and bs * W <= 64
         # the GEMM-prologue norm path (off by default: it would not match the split-K epilogue path bit for bit)
-        if own and bs * W <= self.fuse_norm_rows and c.hidden % 512 == 0 and c.hidden <= 1536:
-            return self._forward_fused(b, n_causal, sl, pt, pos_delta, mkl)
-        K.rmsnorm(b.h, self.n_in[0], b.x, c.rms_eps)
+        fused = own and bs * W <= self.fuse_norm_rows and c.hidden % 512 == 0 and c.hidden <= 1536
+        if emb is None and ids.dtype == torch.int32 and ids.is_contiguous() and not fused:
+            K.embed_rmsnorm(self.embed, ids, self.n_in[0], b.h, b.x, c.rms_eps)   # lookup + first input norm
+        else:
+            if emb is not None:
+                b.h.copy_(emb.view(bs * W, c.hidden))
+            else:
+                torch.index_select(self.embed, 0, ids.reshape(-1), out=b.h)
+            if fused:
+                return self._forward_fused(b, n_causal, sl, pt, pos_delta, mkl)
+            K.rmsnorm(b.h, self.n_in[0], b.x, c.rms_eps)
         if own:
             return self._forward_own(b, n_causal, sl, pt, pos_delta, mkl)
         # more than 64 rows (or gemm="torch"): hipBLASLt GEMMs and the separate norm kernels
@@ -324,7 +328,10 @@ class SelfSpecDecoder:
         Kw = bd + 1
         dev = eng.device
         i32 = dict(dtype=torch.int32, device=dev)
-        self.st = RoundState(bs=bs, K=Kw, x0=torch.zeros(bs, **i32), win=torch.full((bs, Kw), mask_id, **i32),
+        win = torch.full((bs, Kw), mask_id, **i32)
+        # at bs = 1 the boundary token lives in the draft window's first column, where the verify argmax writes it
+        x0 = win[:, 0] if bs == 1 else torch.zeros(bs, **i32)
+        self.st = RoundState(bs=bs, K=Kw, x0=x0, win=win,
                              am=torch.zeros(bs, Kw, **i32), tgt=torch.zeros(bs, Kw, **i32),
                              acc=torch.zeros(bs, **i32), packed=torch.zeros(bs, Kw + 2, **i32),
                              slots=torch.zeros(bs, Kw, **i32), log=torch.zeros(max_rounds, bs, Kw + 2, **i32),
@@ -339,7 +346,7 @@ class SelfSpecDecoder:
         self.log_tgt = torch.zeros(max_rounds, bs, Kw, **i32)   # every round's verify argmax
         self.ar_b = eng.bufs(bs, 1)
         self.ar_tgt = torch.zeros(bs, 1, **i32)
-        self.ar_ids = torch.zeros(bs, 1, **i32)
+        self.ar_ids = self.st.x0.view(bs, 1)        # the AR step's input is the boundary token itself
         self.ar_log = torch.zeros(max_rounds, bs, **i32)
         self.ar_ctr = torch.zeros(1, dtype=torch.int64, device=dev)
         self.g_round = None
@@ -350,7 +357,8 @@ class SelfSpecDecoder:
         """One full-draft round. ``after_draft`` (optional, device ops only) runs between the x0 commit and the
         verify forward and may rewrite the verify window ``st.am[:, 1:]`` (the planted-acceptance measurement)."""
         e, s = self.eng, self.st
-        s.win[:, 0].copy_(s.x0)
+        if self.bs > 1:
+            s.win[:, 0].copy_(s.x0)
         lg = e.forward(self.draft_b, ids=s.win, n_causal=1, pos_delta=self.pos_delta)
         e.argmax(lg, s.am, flags=self.f_draft)                              # a0, d_1..d_B
         e.commit(self.draft_b, n_add=1)                                     # x0's K/V (causal row 0): S += 1
@@ -378,21 +386,15 @@ class SelfSpecDecoder:
         e.argmax(lg, s.tgt, window=s.am, accept_len=s.acc, next_x0=s.x0, packed=s.packed, flags=self.f_verify)
         e.commit(self.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)       # a0, d_1..d_acc: S += acc + 1
         # the log index is clamped on the device, so rounds beyond the log's capacity rewrite its last row
-        li = s.ctr.clamp(max=s.log.shape[0] - 1)
-        s.log.index_copy_(0, li, s.packed.unsqueeze(0))
-        self.log_am.index_copy_(0, li, s.am.unsqueeze(0))
-        self.log_tgt.index_copy_(0, li, s.tgt.unsqueeze(0))
-        s.ctr.add_(1)
+        K.log_append(s.ctr, [(s.packed, s.log), (s.am, self.log_am), (s.tgt, self.log_tgt)])
 
     def ar_step(self):
         e = self.eng
-        self.ar_ids.copy_(self.st.x0.view(self.bs, 1))
         lg = e.forward(self.ar_b, ids=self.ar_ids, n_causal=None, pos_delta=self.pos_delta)
-        e.argmax(lg, self.ar_tgt)
+        # a one-row window: accept length 0, so next_x0 = the argmax itself (written over the input token)
+        e.argmax(lg, self.ar_tgt, window=self.ar_ids, next_x0=self.st.x0)
         e.commit(self.ar_b, n_add=1)
-        self.st.x0.copy_(self.ar_tgt[:, 0])
-        self.ar_log.index_copy_(0, self.ar_ctr.clamp(max=self.ar_log.shape[0] - 1), self.ar_tgt.view(1, self.bs))
-        self.ar_ctr.add_(1)
+        K.log_append(self.ar_ctr, [(self.ar_tgt.view(self.bs), self.ar_log)])
 
     def capture(self):
         """Capture one round and one AR step as HIP graphs (call after one eager warm-up of each)."""

@@ -206,6 +206,22 @@ def kv_meta(req_to_token, req_pool_indices, seq_lens, kv_indptr, kv_indices, *, 
                             _stream()), "gss_kv_meta")
 
 
+def log_append(ctr, pairs):
+    """Row min(ctr, capacity - 1) of each log gets its source's contents, then ctr += 1 (gss_log_append).
+    ctr int64 [1]; pairs: up to three (src int32, log int32 [capacity, *src.shape])."""
+    _need(ctr, torch.int64, "ctr", (1,))
+    if not 1 <= len(pairs) <= 3:
+        raise ValueError("one to three logs")
+    cap = pairs[0][1].shape[0]
+    args = []
+    for src, log in pairs:
+        _need(src, torch.int32, "src")
+        _need(log, torch.int32, "log", (cap,) + tuple(src.shape))
+        args += [_ptr(src), _ptr(log), src.numel()]
+    args += [None, None, 0] * (3 - len(pairs))
+    check(lib().gss_log_append(_ptr(ctr), cap, *args, _stream()), "gss_log_append")
+
+
 def rope_stage(qkv, seq_lens, inv_freq, q, k_win, v_win, *, pos_offset=0, pos_delta=None, rot_dim: int):
     """qkv [bs*W, (Hq+2Hkv)*D] bf16 (row stride qkv.stride(0)); q [bs, W, Hq, D]; k_win/v_win [bs, W, Hkv, D]."""
     bs, W, Hq, D = q.shape
@@ -236,6 +252,18 @@ def rope_stage_mrope(qkv, positions, inv_freq, q, k_win, v_win, *, sections, rot
 def rmsnorm(x, w, out, eps):
     rows, H = x.shape
     check(lib().gss_rmsnorm(_ptr(x), _ptr(w), _ptr(out), rows, H, float(eps), _stream()), "gss_rmsnorm")
+
+
+def embed_rmsnorm(table, ids, w, h, x, eps):
+    """h = table[ids] (rows = ids.numel()), x = rmsnorm(h) * w; ids int32, contiguous."""
+    V, H = table.shape
+    _need(table, torch.bfloat16, "table")
+    _need(ids, torch.int32, "ids")
+    rows = ids.numel()
+    _need(h, torch.bfloat16, "h", (rows, H))
+    _need(x, torch.bfloat16, "x", (rows, H))
+    check(lib().gss_embed_rmsnorm(_ptr(table), _ptr(ids), V, _ptr(w), _ptr(h), _ptr(x), rows, H, float(eps),
+                                  _stream()), "gss_embed_rmsnorm")
 
 
 def add_rmsnorm(a, w_post, h, w_next, x, eps):

@@ -146,6 +146,7 @@ int gss_unmask_step(const void* logits, int dtype, int64_t ld_row, int bs, int W
  * written; the staging is overwritten by the next forward). slots (optional, [bs, W]) receives the slot index
  * page_table[b][pos / page] * page + pos % page of each committed row, -1 for the rest.
  * Window/page tensors of layer l start at k_win + l * win_layer_stride (elements), k_pages + l * page_layer_stride.
+ * page must be 16 and Hkv * 16 * (D + 2) * 2 bytes at most 64 KiB (GSS_ERR_UNSUPPORTED otherwise).
  * Workspace: gss_kv_commit_workspace_size bytes (per-sequence counters), zeroed once after allocation.
  */
 int gss_kv_commit_workspace_size(int bs, size_t* bytes);
@@ -249,6 +250,13 @@ int gss_kv_meta(const int32_t* req_to_token, int64_t r2t_stride, int64_t n_req, 
                 const int64_t* seq_lens, int extra, int32_t* kv_indptr, int32_t* kv_indices,
                 int64_t kv_indices_cap, int bs, gss_stream_t stream);
 
+/* gss_log_append: the device-side round history of the graph-replayed decode loop (no counterpart in the
+ * reference, which reads every round back to the host: src/fast_sampling.py:581-583). Row li = min(*ctr,
+ * capacity - 1) of each log s (int32 [capacity, len_s]) receives src_s[0 .. len_s), then *ctr += 1. Up to three
+ * logs; a NULL src skips its log. One launch of one workgroup. */
+int gss_log_append(int64_t* ctr, int capacity, const int32_t* src0, int32_t* log0, int len0, const int32_t* src1,
+                   int32_t* log1, int len1, const int32_t* src2, int32_t* log2, int len2, gss_stream_t stream);
+
 /* ---------------------------------------------------------------- decoder-layer helpers -------------------------
  * Fused elementwise pieces of the GLM text decoder layer (transformers GlmOcrTextDecoderLayer, which the reference
  * calls through src/fast_sampling.py:89-102). bf16 in and out; fp32 inside; every step rounds to bf16 where the
@@ -273,6 +281,12 @@ int gss_rope_stage_mrope(const void* qkv, int64_t ld_qkv, const int32_t* positio
 
 /* out = rmsnorm(x) * w  (GlmOcrRMSNorm), rows x H. */
 int gss_rmsnorm(const void* x, const void* w, void* out, int rows, int H, float eps, gss_stream_t stream);
+
+/* h[r] = table[ids[r]] (embed_tokens, src/fast_sampling.py:484), x[r] = rmsnorm(h[r]) * w: the embedding lookup of
+ * a window and the first layer's input norm in one launch (bit-identical to the lookup followed by gss_rmsnorm).
+ * table bf16 [V, H], ids int32 [rows]; an id outside [0, V) gives a zero row. */
+int gss_embed_rmsnorm(const void* table, const int32_t* ids, int V, const void* w, void* h, void* x, int rows,
+                      int H, float eps, gss_stream_t stream);
 
 /* h = h + rmsnorm(a) * w_post;  x = rmsnorm(h) * w_next   (sandwich-norm residual, then the next norm). */
 int gss_add_rmsnorm(const void* a, const void* w_post, void* h, const void* w_next, void* x, int rows, int H,

@@ -84,3 +84,32 @@ def test_norms_and_silu(cuda):
     torch.cuda.synchronize()
     gate, up = gu.chunk(2, -1)
     ulp_close(act, up * torch.nn.functional.silu(gate))
+
+
+@pytest.mark.parametrize("rows,H", [(17, 1536), (1, 1536), (33, 256), (5, 64)])
+def test_embed_rmsnorm_equals_lookup_then_norm(cuda, rows, H):
+    """The fused lookup + first input norm equals index_select followed by gss_rmsnorm bit for bit; ids outside the
+    table give zero rows (h and x)."""
+    from gravityocr_amd.kernels import embed_rmsnorm, rmsnorm
+    print(f"embed_rmsnorm rows={rows} H={H}", flush=True)
+    g = torch.Generator().manual_seed(rows * 7 + H)
+    V, eps = 4096, 1e-5
+    table = torch.randn(V, H, generator=g).bfloat16().to(cuda)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16().to(cuda)
+    ids = torch.randint(0, V, (rows,), generator=g, dtype=torch.int32)
+    ids[0] = V - 1
+    if rows > 2:
+        ids[1], ids[2] = -1, V          # out of range: zero rows
+    ids = ids.to(cuda)
+    h = torch.full((rows, H), 7.0, dtype=torch.bfloat16, device=cuda)
+    x = torch.full((rows, H), 7.0, dtype=torch.bfloat16, device=cuda)
+    embed_rmsnorm(table, ids, w, h, x, eps)
+    valid = (ids >= 0) & (ids < V)
+    h_ref = torch.zeros(rows, H, dtype=torch.bfloat16, device=cuda)
+    h_ref[valid] = table[ids[valid].long()]
+    x_ref = torch.empty_like(h_ref)
+    rmsnorm(h_ref, w, x_ref, eps)
+    torch.cuda.synchronize()
+    assert torch.equal(h, h_ref)
+    assert torch.equal(x, x_ref)
+    assert not x[~valid].any()

@@ -61,3 +61,25 @@ def test_kv_meta_matches_oracle(cuda, bs, extra):
     np.testing.assert_array_equal(ptr.cpu().numpy(), w_ptr)
     np.testing.assert_array_equal(idx[:len(w_idx)].cpu().numpy(), w_idx)
     assert bool((idx[len(w_idx):] == -9).all())
+
+
+def test_log_append_rows_clamp_and_counter(cuda):
+    """gss_log_append writes row min(ctr, capacity - 1) of every log and advances the counter by one per call;
+    calls beyond the capacity rewrite the last row."""
+    from gravityocr_amd.kernels import log_append
+    cap, bs, K = 4, 3, 17
+    ctr = torch.zeros(1, dtype=torch.int64, device=cuda)
+    logs = [torch.full((cap, bs, K + 2), -1, dtype=torch.int32, device=cuda),
+            torch.full((cap, bs, K), -1, dtype=torch.int32, device=cuda),
+            torch.full((cap, bs), -1, dtype=torch.int32, device=cuda)]
+    want = [torch.full(t.shape, -1, dtype=torch.int32) for t in logs]
+    for call in range(6):
+        srcs = [torch.arange(t[0].numel(), dtype=torch.int32, device=cuda).view(t[0].shape) * 10 + call for t in logs]
+        pairs = list(zip(srcs, logs))[: 1 + call % 3]
+        log_append(ctr, pairs)
+        for i, (src, _) in enumerate(pairs):
+            want[i][min(call, cap - 1)] = src.cpu()
+    torch.cuda.synchronize()
+    assert int(ctr.item()) == 6
+    for t, w in zip(logs, want):
+        assert torch.equal(t.cpu(), w)
