@@ -63,12 +63,24 @@ struct GemmParams {
 
 constexpr int MAX_NW = 12;  // waves per workgroup (768 threads: 168 VGPRs per lane)
 constexpr size_t MAX_LDS = 160 * 1024;  // LDS per workgroup on gfx950
+constexpr size_t MAX_DYN_LDS = MAX_LDS - 1024;  // dynamic part of it (the kernels' static LDS is a few bytes)
 
 // Wave w owns the contiguous k-steps [w*ksw, (w+1)*ksw) and walks them in passes of UNR steps; every weight and
 // activation load of a pass is issued before the pass's first MFMA, so each wave keeps UNR*(FT+NT) 16-byte loads
 // in flight and a workgroup needs ceil(ksw / UNR) HBM round trips for its whole weight slice.
 enum { PRO_NONE = 0, PRO_ADDNORM = 1 };
 constexpr int XPAD = 8;  // bf16 elements of padding per LDS activation row (spreads rows over the LDS banks)
+
+typedef __attribute__((address_space(1))) void gvoid_t;  // global memory (direct-to-LDS load source)
+typedef __attribute__((address_space(3))) void lvoid_t;  // LDS (its destination)
+
+// Activation staging (XS): a vector memory instruction costs the CU's address unit about the same whatever its
+// active lanes, so a fragment load of a partly filled row tile (17 rows: the second tile has one live row) costs as
+// much as a full one. Instead each wave copies its own k-range of all M rows into LDS with full-lane direct-to-LDS
+// loads (64 x 16-byte chunks per instruction) and reads its B fragments from there. Chunk c (16 bytes) of row r of
+// the wave's range sits at slot r * CPR + (c ^ (r & 15)), CPR = 16-byte chunks per row (a multiple of 16): the 16
+// rows of one fragment read land in 16 different bank groups.
+GSS_DEV int xs_slot(int r, int c, int cpr) { return r * cpr + (c ^ (r & 15)); }
 
 // Prologue: the normalized activation rows x (bf16) go to LDS. One wavefront per row; lane l owns the E = Kd/64
 // consecutive elements [l*E, (l+1)*E); the arithmetic and rounding points are gss_add_rmsnorm's, so the fused and
@@ -244,9 +256,11 @@ GSS_DEV void gemm_epilogue(const GemmParams& p, int f0, int f, int n, floatx4_t 
   }
 }
 
-template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8, bool POST = false>
+template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8, bool POST = false, bool XS = false>
 __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw) {
-  extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD]
+  // LDS: [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD] or (XS) per wave [M][ksw * 4]
+  // 16-byte chunks of its k-range
+  extern __shared__ floatx4_t red[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int f0 = blockIdx.x * FT * 16;
@@ -277,6 +291,21 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   }
 
   uint16_t* xs = reinterpret_cast<uint16_t*>(red + NW * FT * NT * 64);
+  const int cpr = ksw * 4;
+  uint16_t* xw = xs + wv * p.M * cpr * 8;  // XS: this wave's staged rows
+  if constexpr (XS) {
+    // one pass (ksw <= UNR): rows 0..M-1, k-steps [s_beg, s_end) -> LDS, issued before the weight loads below
+    const int n_slots = p.M * cpr, live_chunks = (s_end - s_beg) * 4;
+    const uint16_t* xbase = p.x + static_cast<int64_t>(s_beg) * 32;
+#pragma unroll 1
+    for (int j = 0; j * 64 < n_slots; ++j) {
+      const int q = j * 64 + lane;
+      const int r = q / cpr, c = (q % cpr) ^ (r & 15);
+      if (q < n_slots && c < live_chunks)
+        __builtin_amdgcn_global_load_lds((gvoid_t*)(xbase + static_cast<int64_t>(r) * p.ldx + c * 8),
+                                         (lvoid_t*)(xw + j * 512), 16, 0, 0);
+    }
+  }
   // PRO_ADDNORM runs exactly one pass on every wave (the prologue has a workgroup barrier)
   const int sp_end = PRO == PRO_ADDNORM ? s_beg + 1 : s_end;
   for (int sp = s_beg; sp < sp_end; sp += UNR) {
@@ -303,6 +332,18 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
           xb[u][n] = (s < s_end && xlive[n])
                          ? *reinterpret_cast<const u32x4_t*>(xs + (n * 16 + l16) * (p.Kd + XPAD) + s * 32 + g4 * 8)
                          : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    } else if constexpr (XS) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows (and the weights) have landed
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) {
+          const int r = n * 16 + l16;
+          xb[u][n] = (sp + u < s_end && xlive[n])
+                         ? *reinterpret_cast<const u32x4_t*>(xw + xs_slot(r, u * 4 + g4, cpr) * 8)
+                         : u32x4_t{0u, 0u, 0u, 0u};
+        }
       }
     } else {
 #pragma unroll
@@ -522,6 +563,15 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
 // the most k splits over workgroups (1 = none).
 int g_max_nw = MAX_NW, g_ft = 0, g_max_ksplit = 2;
 int g_stream_wgs = 0;  // workgroups of the persistent GEMM (0: the device's CU count)
+constexpr bool kStageX = true;  // stage the activations through LDS where it applies (gemm_kernel)
+
+// Dynamic LDS beyond the default 64 KB for kernel K (once per process, before its first launch).
+template <auto K>
+bool allow_full_lds() {
+  static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(K),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, MAX_DYN_LDS) == hipSuccess;
+  return ok;
+}
 
 // workgroups of the persistent kernel: one per CU of the current device (queried once)
 int stream_wgs() {
@@ -612,13 +662,28 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
         return gss_launch_status();
       }
     }
+    // activations staged in LDS when a wave's k-range is one pass and the rows fit (same arithmetic either way)
+    const size_t lds_xs = lds + static_cast<size_t>(nw) * p.M * ksw * 64;
+    const bool xs = kStageX && lds_xs <= MAX_DYN_LDS;
     if constexpr (FT + NT <= 3) {
       if (ksw % 8 == 0) {
-        hipLaunchKernelGGL((gemm_kernel<FT, NT, 8, EPI, PRO_NONE, 8, POST>), grid, block, lds, st, p, ksw);
+        constexpr auto kx = gemm_kernel<FT, NT, 8, EPI, PRO_NONE, 8, POST, true>;
+        if (xs && ksw == 8) {
+          if (!allow_full_lds<kx>()) return GSS_ERR_LAUNCH;
+          hipLaunchKernelGGL(kx, grid, block, lds_xs, st, p, ksw);
+        } else {
+          hipLaunchKernelGGL((gemm_kernel<FT, NT, 8, EPI, PRO_NONE, 8, POST>), grid, block, lds, st, p, ksw);
+        }
         return gss_launch_status();
       }
     }
-    hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO_NONE, 8, POST>), grid, block, lds, st, p, ksw);
+    constexpr auto kx4 = gemm_kernel<FT, NT, 4, EPI, PRO_NONE, 8, POST, true>;
+    if (xs && ksw == 4) {
+      if (!allow_full_lds<kx4>()) return GSS_ERR_LAUNCH;
+      hipLaunchKernelGGL(kx4, grid, block, lds_xs, st, p, ksw);
+    } else {
+      hipLaunchKernelGGL((gemm_kernel<FT, NT, 4, EPI, PRO_NONE, 8, POST>), grid, block, lds, st, p, ksw);
+    }
     return gss_launch_status();
   }
 }
