@@ -32,6 +32,8 @@ SIGNATURES = {
     "gss_gemm_set_policy": ([_i, _i, _i], _i),
     "gss_gemm_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p, _p, _sz, _p], _i),
+    "gss_gemm_parts_count": ([_i, _i, ctypes.POINTER(ctypes.c_int)], _i),
+    "gss_gemm_parts": ([_p, _i64, _p, _i64, _p, _i, _i, _i, _p], _i),
     "gss_gemm_swiglu": ([_p, _i64, _p, _p, _i64, _p, _i, _i, _i, _p, _sz, _p], _i),
     "gss_gemm_rope_stage": ([_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz,
                              _p], _i),
@@ -40,6 +42,7 @@ SIGNATURES = {
     "gss_rmsnorm": ([_p, _p, _p, _i, _i, _f, _p], _i),
     "gss_embed_rmsnorm": ([_p, _p, _i, _p, _p, _p, _i, _i, _f, _p], _i),
     "gss_add_rmsnorm": ([_p, _p, _p, _p, _p, _i, _i, _f, _p], _i),
+    "gss_add_rmsnorm_parts": ([_p, _i, _p, _p, _p, _p, _i, _i, _f, _p], _i),
     "gss_silu_mul": ([_p, _i64, _p, _i, _i, _p], _i),
 }
 
@@ -54,7 +57,8 @@ class NormEpilogue(ctypes.Structure):
 class NormPrologue(ctypes.Structure):
     """gss_norm_prologue (include/gss.h)."""
     _fields_ = [("a", ctypes.c_void_p), ("h_in", ctypes.c_void_p), ("h_out", ctypes.c_void_p),
-                ("w_post", ctypes.c_void_p), ("w_next", ctypes.c_void_p), ("eps", ctypes.c_float)]
+                ("w_post", ctypes.c_void_p), ("w_next", ctypes.c_void_p), ("eps", ctypes.c_float),
+                ("a_parts", ctypes.c_void_p), ("n_parts", ctypes.c_int)]
 
 
 _LIB = None

@@ -16,11 +16,13 @@
 //   EPI_ROPE    N = (Hq + 2 Hkv) * D q|k|v projection -> RoPE on q and k (interleaved pairs of the first rot_dim dims,
 //               position = seq_lens[b] + pos_delta[b] + w), written as q [bs, W, Hq, D] and window K/V [bs, W, Hkv, D]
 //   EPI_SWIGLU  N = 2F with gate/up rows interleaved (row 2i = gate_i, 2i+1 = up_i) -> act[M, F] = up * silu(gate)
+//   EPI_PARTS   the k splits' fp32 partial sums [S][M][N], summed in split order (then rounded to bf16) by the
+//               consumer: no handoff between the splits, the kernel boundary orders them
 #include "gss_common.h"
 
 namespace {
 
-enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_SWIGLU = 2 };
+enum { EPI_PLAIN = 0, EPI_ROPE = 1, EPI_SWIGLU = 2, EPI_PARTS = 3 };
 
 struct GemmParams {
   const uint16_t* x;
@@ -42,6 +44,8 @@ struct GemmParams {
   // prologue (PRO_ADDNORM): x = rmsnorm(h') * w_next with h' = h_in + rmsnorm(a) * w_post (a == nullptr: h' = h_in);
   // workgroup (0, 0) stores h' to h_out (never h_in: other workgroups still read it)
   const uint16_t* pa;
+  const float* pa_parts;  // or a given as n_parts fp32 partial sums [n_parts][M][Kd] (a = bf16 of their sum)
+  int n_parts;
   const uint16_t* h_in;
   uint16_t* h_out;
   const uint16_t* w_post;
@@ -82,6 +86,11 @@ typedef __attribute__((address_space(3))) void lvoid_t;  // LDS (its destination
 // rows of one fragment read land in 16 different bank groups.
 GSS_DEV int xs_slot(int r, int c, int cpr) { return r * cpr + (c ^ (r & 15)); }
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory operations are outstanding and
+// leaves the other counters free: vmcnt[3:0] in bits 3:0, expcnt 7 in bits 6:4, lgkmcnt 15 in bits 11:8. The
+// builtin form lets the compiler's own wait counting see the direct-to-LDS loads complete.
+constexpr int waitcnt_vm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
 // Prologue: the normalized activation rows x (bf16) go to LDS. One wavefront per row; lane l owns the E = Kd/64
 // consecutive elements [l*E, (l+1)*E); the arithmetic and rounding points are gss_add_rmsnorm's, so the fused and
 // unfused paths agree bit for bit.
@@ -101,7 +110,24 @@ GSS_DEV void addnorm_row(const GemmParams& p, int row, int lane, uint16_t* xs, b
       wn[c * 8 + 2 * e] = __uint_as_float(qn[e] << 16);
       wn[c * 8 + 2 * e + 1] = __uint_as_float(qn[e] & 0xffff0000u);
     }
-    if (p.pa != nullptr) {
+    if (p.pa_parts != nullptr) {
+      // a = bf16 of the partial sums, added in part order (gss_add_rmsnorm_parts' arithmetic)
+      const float* pp = p.pa_parts + off + c * 8;
+      const int64_t pstride = static_cast<int64_t>(p.M) * KD;
+      floatx4_t s0 = *reinterpret_cast<const floatx4_t*>(pp), s1 = *reinterpret_cast<const floatx4_t*>(pp + 4);
+      for (int k = 1; k < p.n_parts; ++k) {
+        s0 += *reinterpret_cast<const floatx4_t*>(pp + k * pstride);
+        s1 += *reinterpret_cast<const floatx4_t*>(pp + k * pstride + 4);
+      }
+      const u32x4_t qp = *reinterpret_cast<const u32x4_t*>(p.w_post + lane * E + c * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        av[c * 8 + e] = round_bf16(s0[e]);
+        av[c * 8 + 4 + e] = round_bf16(s1[e]);
+        wp[c * 8 + 2 * e] = __uint_as_float(qp[e] << 16);
+        wp[c * 8 + 2 * e + 1] = __uint_as_float(qp[e] & 0xffff0000u);
+      }
+    } else if (p.pa != nullptr) {
       const u32x4_t qa = *reinterpret_cast<const u32x4_t*>(p.pa + off + c * 8);
       const u32x4_t qp = *reinterpret_cast<const u32x4_t*>(p.w_post + lane * E + c * 8);
 #pragma unroll
@@ -113,7 +139,7 @@ GSS_DEV void addnorm_row(const GemmParams& p, int row, int lane, uint16_t* xs, b
       }
     }
   }
-  if (p.pa != nullptr) {
+  if (p.pa != nullptr || p.pa_parts != nullptr) {
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) ss += av[e] * av[e];
@@ -334,7 +360,7 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
                          : u32x4_t{0u, 0u, 0u, 0u};
       }
     } else if constexpr (XS) {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged rows (and the weights) have landed
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the staged rows (and the weights) have landed
 #pragma unroll
       for (int u = 0; u < UNR; ++u) {
 #pragma unroll
@@ -386,6 +412,18 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   auto live = [&](int f, int n) { return n * 16 + l16 < p.M && f0 + f * 16 + g4 * 4 < p.N; };
   __shared__ int last_flag;
 
+  if constexpr (EPI == EPI_PARTS) {
+    // this split's fp32 partial sums, plain stores (read by a later kernel)
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        if ((f * NT + n) % NW == wv && live(f, n))
+          *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) +
+                                        (static_cast<int64_t>(ks) * p.M + n * 16 + l16) * p.ldy + f0 + f * 16 +
+                                        g4 * 4) = reduced(f, n);
+    return;
+  }
   if (p.ksplit == 1) {
 #pragma unroll
     for (int f = 0; f < FT; ++f)
@@ -603,6 +641,13 @@ int gemm_ksplit(int n_tiles, int ksteps) {
 
 int gemm_ft(int N) { return (g_ft == 1 || (g_ft == 0 && N / 16 <= 2048)) ? 1 : 2; }
 
+// k splits of the partial-sum output (EPI_PARTS): up to 2, as many as keep the column tiles x splits within one
+// workgroup per CU, each split at least 4 k-steps. A function of the weight shape only (the reduction order).
+int gemm_parts_split(int n_tiles, int ksteps) {
+  const int ks = max(1, min(2, stream_wgs() / max(1, n_tiles)));
+  return ksteps / ks >= 4 ? ks : 1;
+}
+
 size_t gemm_ws_bytes(int M, int N, int Kd) {
   const int ft = gemm_ft(N), n_tiles = (N + ft * 16 - 1) / (ft * 16);
   const int ks = gemm_ksplit(n_tiles, Kd / 32);
@@ -613,9 +658,9 @@ template <int FT, int NT, int EPI, int PRO, bool POST>
 int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
   const int ksteps = p.Kd / 32;
   const int n_tiles = (p.N + FT * 16 - 1) / (FT * 16);
-  p.ksplit = gemm_ksplit(n_tiles, ksteps);
+  p.ksplit = EPI == EPI_PARTS ? gemm_parts_split(n_tiles, ksteps) : gemm_ksplit(n_tiles, ksteps);
   p.kps = (ksteps + p.ksplit - 1) / p.ksplit;
-  if (p.ksplit > 1 || POST) {
+  if ((p.ksplit > 1 && EPI != EPI_PARTS) || POST) {
     if (n_tiles > CTR_TILES) return GSS_ERR_UNSUPPORTED;
     const size_t need = CTR_BYTES + (p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * p.M * p.N * sizeof(float) : 0);
     if (!ws || ws_bytes < need) return GSS_ERR_WORKSPACE;
@@ -657,7 +702,7 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
       // more column tiles than CUs and one load pass per tile (a function of N and Kd only, so every row count
       // takes the same kernel): the persistent kernel, one workgroup per CU walking the tiles
       const int G = stream_wgs();
-      if (p.ksplit == 1 && ksw <= 4 && n_tiles > G) {
+      if (EPI != EPI_PARTS && p.ksplit == 1 && ksw <= 4 && n_tiles > G) {
         hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI>), dim3(G), block, lds, st, p, ksw, n_tiles);
         return gss_launch_status();
       }
@@ -730,6 +775,8 @@ int gemm_entry(GemmParams& p, int epi, void* ws, size_t ws_bytes, hipStream_t st
   }
   if (pro) {
     if (!p.w_next || (p.pa && !p.w_post) || p.h_out == p.h_in) return GSS_ERR_ARG;
+    if (p.pa_parts && (p.pa || !p.w_post || p.n_parts < 1 || (reinterpret_cast<uintptr_t>(p.pa_parts) & 15u)))
+      return GSS_ERR_ARG;
     if (p.Kd % 512 != 0) return GSS_ERR_UNSUPPORTED;  // 8-element chunks per lane
     if ((reinterpret_cast<uintptr_t>(p.h_in) | reinterpret_cast<uintptr_t>(p.pa) |
          reinterpret_cast<uintptr_t>(p.h_out) | reinterpret_cast<uintptr_t>(p.w_next) |
@@ -744,6 +791,7 @@ int gemm_entry(GemmParams& p, int epi, void* ws, size_t ws_bytes, hipStream_t st
   switch (epi) {
     case EPI_PLAIN: return launch_epi<EPI_PLAIN, PRO_NONE, false>(p, ws, ws_bytes, st);
     case EPI_SWIGLU: return launch_epi<EPI_SWIGLU, PRO_NONE, false>(p, ws, ws_bytes, st);
+    case EPI_PARTS: return launch_epi<EPI_PARTS, PRO_NONE, false>(p, ws, ws_bytes, st);
     default: return launch_epi<EPI_ROPE, PRO_NONE, false>(p, ws, ws_bytes, st);
   }
 }
@@ -757,6 +805,8 @@ void set_prologue(GemmParams& p, const gss_norm_prologue* pro) {
   p.w_post = static_cast<const uint16_t*>(pro->w_post);
   p.w_next = static_cast<const uint16_t*>(pro->w_next);
   p.eps = pro->eps;
+  p.pa_parts = pro->a_parts;
+  p.n_parts = pro->n_parts;
 }
 
 }  // namespace
@@ -793,6 +843,30 @@ extern "C" int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro
     p.post_eps = post->eps;
   }
   return gemm_entry(p, EPI_PLAIN, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int gss_gemm_parts_count(int N, int Kd, int* n_parts) {
+  if (!n_parts || N <= 0 || Kd <= 0 || N % 16 != 0 || Kd % 32 != 0) return GSS_ERR_ARG;
+  const int ft = gemm_ft(N);
+  *n_parts = gemm_parts_split((N + ft * 16 - 1) / (ft * 16), Kd / 32);
+  return GSS_OK;
+}
+
+extern "C" int gss_gemm_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, float* parts, int M, int N,
+                              int Kd, gss_stream_t stream) {
+  if (!parts || (reinterpret_cast<uintptr_t>(parts) & 15u)) return GSS_ERR_ARG;
+  GemmParams p = {};
+  p.x = static_cast<const uint16_t*>(x);
+  p.ldx = ldx;
+  p.w = static_cast<const uint16_t*>(w);
+  p.ldw = ldw;
+  p.y = parts;
+  p.ldy = N;
+  p.M = M;
+  p.N = N;
+  p.Kd = Kd;
+  p.out_f32 = 1;
+  return gemm_entry(p, EPI_PARTS, nullptr, 0, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int gss_gemm_swiglu(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_gu_interleaved,

@@ -40,6 +40,10 @@ class _Bufs:
         self.q = torch.empty(bs, W, c.n_heads, c.head_dim, dtype=bf, device=dev)
         self.o = torch.empty(bs, W, c.n_heads, c.head_dim, dtype=bf, device=dev)
         self.a = torch.empty(rows, c.hidden, dtype=bf, device=dev)
+        # fp32 partial sums of o_proj and down_proj (gemm_parts), summed by the norm that follows
+        self.ap_o = torch.empty(K.gemm_parts_count(c.hidden, c.n_heads * c.head_dim), rows, c.hidden,
+                                dtype=torch.float32, device=dev)
+        self.ap_d = torch.empty(K.gemm_parts_count(c.hidden, c.ffn), rows, c.hidden, dtype=torch.float32, device=dev)
         self.gu = torch.empty(rows, 2 * c.ffn, dtype=bf, device=dev)
         self.act = torch.empty(rows, c.ffn, dtype=bf, device=dev)
         self.logits = torch.empty(rows, c.vocab, dtype=bf, device=dev)
@@ -65,6 +69,7 @@ class GssEngine:
         # pays: at most 12 rows (one row per wave of the GEMM's 12; the 1-row AR step gains ~21 us per forward, a
         # 17-row round forward loses ~25 us) and a hidden size the prologue supports (a multiple of 512, <= 1536)
         self.fuse_gate_norm = True
+        self.gemm_parts = True    # o_proj / down as k-split partial sums (gemm_parts + the parts norms)
         self.device = torch.device(device)
         self.max_bs, self.max_len, self.max_win = max_bs, max_len, max_win
         dev, bf = self.device, torch.bfloat16
@@ -183,6 +188,19 @@ class GssEngine:
                 K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
                 K.gemm(b.act, self.wdown[l], b.a, workspace=ws,
                        post=dict(h=h, w_post=self.n_pm[l], w_next=nxt, x=b.x, eps=c.rms_eps))
+            elif self.gemm_parts and (c.hidden // 64) % 4 == 0:
+                # o_proj and down as k-split partial sums, added in split order by the norm that follows
+                K.gemm_parts(b.o.view(bs * W, -1), self.wo[l], b.ap_o)
+                if self.fuse_gate_norm and bs * W <= 12 and c.hidden % 512 == 0 and c.hidden <= 1536:
+                    K.gemm_swiglu(None, self.wgu[l], b.act, workspace=ws,
+                                  pro=dict(a_parts=b.ap_o, h_in=h, h_out=h_alt, w_post=self.n_psa[l],
+                                           w_next=self.n_pa[l], eps=c.rms_eps))
+                    h, h_alt = h_alt, h
+                else:
+                    K.add_rmsnorm_parts(b.ap_o, self.n_psa[l], h, self.n_pa[l], b.x, c.rms_eps)
+                    K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
+                K.gemm_parts(b.act, self.wdown[l], b.ap_d)
+                K.add_rmsnorm_parts(b.ap_d, self.n_pm[l], h, nxt, b.x, c.rms_eps)
             else:
                 K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a, workspace=ws)
                 if self.fuse_gate_norm and bs * W <= 12 and c.hidden % 512 == 0 and c.hidden <= 1536:

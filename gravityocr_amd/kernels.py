@@ -288,7 +288,8 @@ def _gemm_args(x, w):
 
 
 def _prologue(pro, M, Kd):
-    """pro = dict(h_in=..., w_next=..., eps=..., a=None, w_post=None, h_out=None) -> (NormPrologue or None)."""
+    """pro = dict(h_in=..., w_next=..., eps=..., a=None, w_post=None, h_out=None, a_parts=None) -> (NormPrologue or
+    None). ``a_parts`` (fp32 [n_parts, M, Kd], from gemm_parts) stands for a = bf16 of the parts' sum."""
     if pro is None:
         return None
     for k in ("h_in", "a", "h_out"):
@@ -299,8 +300,12 @@ def _prologue(pro, M, Kd):
         t = pro.get(k)
         if t is not None:
             _need(t, torch.bfloat16, f"prologue {k}", (Kd,))
+    ap = pro.get("a_parts")
+    if ap is not None:
+        _need(ap, torch.float32, "prologue a_parts", (ap.shape[0], M, Kd))
     return NormPrologue(_ptr(pro.get("a")).value, _ptr(pro["h_in"]).value, _ptr(pro.get("h_out")).value,
-                        _ptr(pro.get("w_post")).value, _ptr(pro["w_next"]).value, float(pro["eps"]))
+                        _ptr(pro.get("w_post")).value, _ptr(pro["w_next"]).value, float(pro["eps"]), _ptr(ap).value,
+                        0 if ap is None else ap.shape[0])
 
 
 def _rows(x, pro):
@@ -357,6 +362,31 @@ def gemm(x, w, y, pro=None, post=None, workspace=None):
     check(lib().gss_gemm(_ptr(x), ldx, None if pr is None else ctypes.byref(pr), _ptr(w), w.stride(0), _ptr(y),
                          y.stride(0), M, N, Kd, dt, None if po is None else ctypes.byref(po), _ptr(ws),
                          ws.numel(), _stream()), "gss_gemm")
+
+
+def gemm_parts_count(N, Kd) -> int:
+    n = ctypes.c_int(0)
+    check(lib().gss_gemm_parts_count(N, Kd, ctypes.byref(n)), "gss_gemm_parts_count")
+    return n.value
+
+
+def gemm_parts(x, w, parts):
+    """parts[s, :M, :N] (fp32, [n_parts, M, N] contiguous, n_parts = gemm_parts_count(N, Kd)): the k splits'
+    partial sums of x @ w^T; y = bf16(parts.sum(0) in part order)."""
+    _gemm_args(x, w)
+    Kd, N = w.shape[1], w.shape[0]
+    M = x.shape[0]
+    _need(parts, torch.float32, "parts", (gemm_parts_count(N, Kd), M, N))
+    check(lib().gss_gemm_parts(_ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(parts), M, N, Kd, _stream()),
+          "gss_gemm_parts")
+
+
+def add_rmsnorm_parts(parts, w_post, h, w_next, x, eps):
+    """gss_add_rmsnorm with a = bf16 of the fp32 parts' sum (parts [n_parts, rows, H])."""
+    rows, H = h.shape
+    _need(parts, torch.float32, "parts", (parts.shape[0], rows, H))
+    check(lib().gss_add_rmsnorm_parts(_ptr(parts), parts.shape[0], _ptr(w_post), _ptr(h), _ptr(w_next), _ptr(x),
+                                      rows, H, float(eps), _stream()), "gss_add_rmsnorm_parts")
 
 
 def gemm_swiglu(x, w_gu_il, act, pro=None, workspace=None):

@@ -178,6 +178,9 @@ typedef struct gss_norm_prologue {
   const void* w_post; /* bf16 [Kd], used with a */
   const void* w_next; /* bf16 [Kd] */
   float eps;
+  const float* a_parts; /* instead of a: fp32 partial sums [n_parts][M][Kd] from gss_gemm_parts (a = bf16 of their
+                           sum in part order, as gss_add_rmsnorm_parts computes it), or NULL */
+  int n_parts;
 } gss_norm_prologue;
 
 /* Launch-shape policy of the three GEMMs (process-wide): at most max_waves (1..12) waves per workgroup splitting
@@ -208,6 +211,17 @@ int gss_gemm_workspace_size(int M, int N, int Kd, size_t* bytes);
 int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w, int64_t ldw, void* y,
              int64_t ldy, int M, int N, int Kd, int out_dtype, const gss_norm_epilogue* post, void* workspace,
              size_t workspace_bytes, gss_stream_t stream);
+
+/* gss_gemm_parts: Y = X W^T (the torch bf16 linear of o_proj / down_proj) left as n_parts fp32 partial sums over
+ * disjoint k ranges, parts [n_parts][M][N] (16-byte aligned); Y = bf16(parts[0] + parts[1] + ...) in part order,
+ * which gss_add_rmsnorm_parts and the a_parts prologue compute. The k splits spread a projection with few column
+ * tiles over twice the CUs without a handoff between them (the next kernel does the sum). n_parts =
+ * gss_gemm_parts_count(N, Kd), a function of the weight shape (and the device's CU count) only: every M uses the
+ * same partition, so rows stay batch invariant. No counterpart in the reference (how its linear is computed). */
+int gss_gemm_parts_count(int N, int Kd, int* n_parts);
+
+int gss_gemm_parts(const void* x, int64_t ldx, const void* w, int64_t ldw, float* parts, int M, int N, int Kd,
+                   gss_stream_t stream);
 
 int gss_gemm_swiglu(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w_gu_interleaved,
                     int64_t ldw, void* act, int M, int F, int Kd, void* workspace, size_t workspace_bytes,
@@ -291,6 +305,11 @@ int gss_embed_rmsnorm(const void* table, const int32_t* ids, int V, const void* 
 /* h = h + rmsnorm(a) * w_post;  x = rmsnorm(h) * w_next   (sandwich-norm residual, then the next norm). */
 int gss_add_rmsnorm(const void* a, const void* w_post, void* h, const void* w_next, void* x, int rows, int H,
                     float eps, gss_stream_t stream);
+
+/* gss_add_rmsnorm with a = bf16(parts[0] + ... + parts[n_parts - 1]) (fp32, added in part order; parts
+ * [n_parts][rows][H], 16-byte aligned, as gss_gemm_parts writes them). H / 64 must be a multiple of 4. */
+int gss_add_rmsnorm_parts(const float* parts, int n_parts, const void* w_post, void* h, const void* w_next, void* x,
+                          int rows, int H, float eps, gss_stream_t stream);
 
 /* out[r, :F] = up * silu(gate) with gu[r] = [gate (F) | up (F)], row stride ld_gu elements (GlmOcrTextMLP). */
 int gss_silu_mul(const void* gu, int64_t ld_gu, void* out, int rows, int F, gss_stream_t stream);

@@ -221,3 +221,77 @@ def test_split_k_shapes_share_one_workspace(cuda, ksplit_policy):
                                                        device=cuda))
             torch.cuda.synchronize()
             assert torch.equal(y1, y2), (rep, n, kd)
+
+
+PARTS_SHAPES = [(17, 1536, 2048), (17, 1536, 4608), (1, 1536, 2048), (1, 1536, 4608), (33, 1536, 2048),
+                (5, 256, 256), (5, 256, 704)]
+
+
+@pytest.mark.parametrize("M,N,Kd", PARTS_SHAPES)
+def test_gemm_parts_parity_and_invariance(cuda, M, N, Kd):
+    """gss_gemm_parts: the fp32 partial sums add up to x @ w^T (fp32 reference, same bound as gss_gemm's fp32
+    output); their bf16 sum is the same for a row alone (M = 1) and inside the batch; where gss_gemm splits k the
+    same way (down_proj: 2 splits of 72 k-steps), bf16(parts[0] + parts[1]) is gss_gemm's output bit for bit."""
+    from gravityocr_amd.kernels import gemm, gemm_parts, gemm_parts_count
+    print(f"gemm_parts M={M} N={N} K={Kd}", flush=True)
+    g = torch.Generator().manual_seed(M * 11 + Kd)
+    x = torch.randn(M, Kd, generator=g).bfloat16().to(cuda)
+    w = (torch.randn(N, Kd, generator=g) * 0.02).bfloat16().to(cuda)
+    S = gemm_parts_count(N, Kd)
+    assert 1 <= S <= 2
+    parts = torch.full((S, M, N), float("nan"), dtype=torch.float32, device=cuda)
+    gemm_parts(x, w, parts)
+    r = ref(x, w)
+    total = parts[0].clone()
+    for k in range(1, S):
+        total += parts[k]
+    torch.cuda.synchronize()
+    scale = float(r.abs().max())
+    assert not torch.isnan(parts).any()
+    assert float((total - r).abs().max()) <= 1e-4 * scale + 1e-5
+    for row in (0, M - 1):
+        p1 = torch.empty(S, 1, N, dtype=torch.float32, device=cuda)
+        gemm_parts(x[row:row + 1].contiguous(), w, p1)
+        torch.cuda.synchronize()
+        assert torch.equal(p1[:, 0], parts[:, row]), row
+    if (N, Kd) == (1536, 4608):
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=cuda)
+        gemm(x, w, y)
+        torch.cuda.synchronize()
+        assert S == 2 and torch.equal(y, (parts[0] + parts[1]).bfloat16())
+
+
+@pytest.mark.parametrize("M", [1, 5, 12, 17])
+def test_norms_on_parts_equal_unfused(cuda, M):
+    """gss_add_rmsnorm_parts == gss_add_rmsnorm on a = bf16(sum of the parts), and the gate_up prologue with a_parts
+    == that norm followed by the plain gate_up GEMM, bit for bit (h updated, x, act)."""
+    from gravityocr_amd.kernels import add_rmsnorm, add_rmsnorm_parts, gemm_parts, gemm_swiglu
+    g = torch.Generator().manual_seed(40 + M)
+    H, F, eps = 1536, 4608, 1e-5
+    o = torch.randn(M, 2048, generator=g).bfloat16().to(cuda)
+    wo = (torch.randn(H, 2048, generator=g) * 0.02).bfloat16().to(cuda)
+    h = torch.randn(M, H, generator=g).bfloat16().to(cuda)
+    wp = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16().to(cuda)
+    wn = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16().to(cuda)
+    wgu = (torch.randn(2 * F, H, generator=g) * 0.02).bfloat16().to(cuda)
+    from gravityocr_amd.kernels import gemm_parts_count
+    parts = torch.empty(gemm_parts_count(H, 2048), M, H, dtype=torch.float32, device=cuda)
+    gemm_parts(o, wo, parts)
+    a = parts[0].clone()
+    for k in range(1, parts.shape[0]):
+        a += parts[k]
+    a = a.bfloat16()
+    h_ref, x_ref = h.clone(), torch.empty_like(h)
+    add_rmsnorm(a, wp, h_ref, wn, x_ref, eps)
+    h1, x1 = h.clone(), torch.empty_like(h)
+    add_rmsnorm_parts(parts, wp, h1, wn, x1, eps)
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h_ref) and torch.equal(x1, x_ref)
+    act_ref = torch.empty(M, F, dtype=torch.bfloat16, device=cuda)
+    gemm_swiglu(x_ref, wgu, act_ref)
+    act = torch.empty_like(act_ref)
+    h_out = torch.empty_like(h)
+    if M <= 12:   # the prologue form the engine uses (at most one row per wave)
+        gemm_swiglu(None, wgu, act, pro=dict(a_parts=parts, h_in=h, h_out=h_out, w_post=wp, w_next=wn, eps=eps))
+        torch.cuda.synchronize()
+        assert torch.equal(act, act_ref) and torch.equal(h_out, h_ref)
