@@ -155,6 +155,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--profile-only", action="store_true", help="skip AR, planted and CPU legs (for rocprof runs)")
+    ap.add_argument("--ar-only", action="store_true", help="only the graph-replayed AR steps (for rocprof runs)")
     ap.add_argument("--attn-only", action="store_true",
                     help="only the draft-attention roofline measurement and the copy calibration (for rocprof runs)")
     ap.add_argument("--attn-batched-only", action="store_true",
@@ -239,6 +240,10 @@ def main():
         ar_tps, ar_us = n_ar / dt, dt / n_ar * 1e6
         ar_tokens = [int(x00)] + dec.ar_log[:n_ar, 0].cpu().tolist()
         log(f"AR: {ar_tps:.1f} tokens/s ({ar_us:.1f} us/token)")
+        if args.ar_only:
+            print(json.dumps({"ar_us_per_token": round(ar_us, 1), "ar_tokens_per_s": round(ar_tps, 2),
+                              "steps": n_ar}), flush=True)
+            return
 
     # ---- calibration: rounds that commit args.tokens (untimed) ---------------------------------------------------
     reset()
