@@ -29,6 +29,9 @@ SIGNATURES = {
     "gss_ss_commit": ([_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _p], _i),
     "gss_kv_meta": ([_p, _i64, _i64, _p, _p, _i, _p, _p, _i64, _i, _p], _i),
     "gss_log_append": ([_p, _i, _p, _p, _i, _p, _p, _i, _p, _p, _i, _p], _i),
+    "gss_penalize_rows": ([_p, _i64, _i, _i, _i, _p, _p, _p], _i),
+    "gss_sample_workspace_size": ([_i, _i, _psz], _i),
+    "gss_sample_rows": ([_p, _i64, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
     "gss_gemm_set_policy": ([_i, _i, _i], _i),
     "gss_gemm_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p, _p, _sz, _p], _i),
@@ -52,6 +55,13 @@ class NormEpilogue(ctypes.Structure):
     """gss_norm_epilogue (include/gss.h)."""
     _fields_ = [("w_post", ctypes.c_void_p), ("h", ctypes.c_void_p), ("w_next", ctypes.c_void_p),
                 ("x", ctypes.c_void_p), ("eps", ctypes.c_float)]
+
+
+class Penalties(ctypes.Structure):
+    """gss_penalties (include/gss.h)."""
+    _fields_ = [("n_order", ctypes.c_int), ("order", ctypes.c_int * 4)] + [
+        (n, ctypes.c_void_p) for n in ("rep_cum", "rep_pen", "pres_cum", "pres_pen", "freq_cum", "freq_pen", "len_out",
+                                       "min_new", "stop_pen", "logit_bias")]
 
 
 class NormPrologue(ctypes.Structure):

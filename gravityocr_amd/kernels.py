@@ -5,7 +5,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import NormEpilogue, NormPrologue, check, lib
+from ._lib import NormEpilogue, NormPrologue, Penalties, check, lib
 
 PAGE = 16
 # the attention kernels' library defaults (gss_attn_set_split_policy, gss_attn_set_wide_min)
@@ -379,6 +379,66 @@ def gemm_parts(x, w, parts):
     _need(parts, torch.float32, "parts", (gemm_parts_count(N, Kd), M, N))
     check(lib().gss_gemm_parts(_ptr(x), x.stride(0), _ptr(w), w.stride(0), _ptr(parts), M, N, Kd, _stream()),
           "gss_gemm_parts")
+
+
+PENALIZERS = {"repetition": 1, "presence": 2, "frequency": 3, "min_new_tokens": 4}
+FILTERS = {"none": 0, "joint": 1, "torch": 2}
+
+
+def penalize_rows(logits, cand, state, order):
+    """In place on fp32 logits [bs*K, V] (dense rows): AR's penalties for every verify row (gss_penalize_rows).
+    cand int32 [bs, K]; state: dict of GPU tensors rep_cum/pres_cum/freq_cum/stop_pen/logit_bias fp32 [bs, V],
+    rep_pen/pres_pen/freq_pen fp32 [bs], len_out/min_new int32 [bs] (what ``order`` uses); order: penalizer names
+    in the orchestrator's order."""
+    bs, K = cand.shape
+    V = logits.shape[1]
+    _need(cand, torch.int32, "cand")
+    if logits.dtype != torch.float32 or not logits.is_cuda or logits.stride(1) != 1 or logits.shape[0] != bs * K:
+        raise ValueError("logits must be fp32 [bs*K, V] on the GPU with dense rows")
+    shapes = dict(rep_cum=(bs, V), pres_cum=(bs, V), freq_cum=(bs, V), stop_pen=(bs, V), logit_bias=(bs, V),
+                  rep_pen=(bs,), pres_pen=(bs,), freq_pen=(bs,), len_out=(bs,), min_new=(bs,))
+    for k, t in state.items():
+        if t is not None:
+            _need(t, torch.int32 if k in ("len_out", "min_new") else torch.float32, k, shapes[k])
+    pen = Penalties()
+    pen.n_order = len(order)
+    for i, name in enumerate(order):
+        pen.order[i] = PENALIZERS[name]
+    for k in shapes:
+        setattr(pen, k, _ptr(state.get(k)).value)
+    check(lib().gss_penalize_rows(_ptr(logits), logits.stride(0), bs, K, V, _ptr(cand), ctypes.byref(pen),
+                                  _stream()), "gss_penalize_rows")
+
+
+def sample_workspace_bytes(bs, K) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib().gss_sample_workspace_size(bs, K, ctypes.byref(n)), "gss_sample_workspace_size")
+    return n.value
+
+
+def sample_rows(logits, bs, K, *, temperature, filter="none", top_k=None, top_p=None, min_p=None, cand=None,
+                coins=None, uniforms, sampled, target=None, accept_len=None, next_x0=None, packed=None,
+                workspace=None):
+    """gss_sample_rows on fp32 logits rows (row b*K + r at logits[b*K + r], any row stride): sample mode (cand
+    None: uniforms [bs, K]) or verify mode (cand int32 [bs, K], coins fp32 [bs, K], uniforms [bs])."""
+    if logits.dtype != torch.float32 or not logits.is_cuda or logits.stride(-1) != 1:
+        raise ValueError("logits must be fp32 on the GPU with dense rows")
+    V = logits.shape[-1]
+    ld = logits.stride(-2) if logits.dim() >= 2 else V
+    for name, t, dt, shp in (("temperature", temperature, torch.float32, (bs,)), ("top_k", top_k, torch.int32, (bs,)),
+                             ("top_p", top_p, torch.float32, (bs,)), ("min_p", min_p, torch.float32, (bs,)),
+                             ("cand", cand, torch.int32, (bs, K)), ("coins", coins, torch.float32, (bs, K)),
+                             ("uniforms", uniforms, torch.float32, (bs,) if cand is not None else (bs, K)),
+                             ("sampled", sampled, torch.int32, (bs, K)), ("target", target, torch.int32, (bs, K)),
+                             ("accept_len", accept_len, torch.int32, (bs,)), ("next_x0", next_x0, torch.int32, (bs,)),
+                             ("packed", packed, torch.int32, (bs, K + 2))):
+        if t is not None:
+            _need(t, dt, name, shp)
+    wsb = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().gss_sample_rows(_ptr(logits), ld, bs, K, V, FILTERS[filter], _ptr(temperature), _ptr(top_k),
+                                _ptr(top_p), _ptr(min_p), _ptr(cand), _ptr(coins), _ptr(uniforms), _ptr(sampled),
+                                _ptr(target), _ptr(accept_len), _ptr(next_x0), _ptr(packed), _ptr(workspace), wsb,
+                                _stream()), "gss_sample_rows")
 
 
 def add_rmsnorm_parts(parts, w_post, h, w_next, x, eps):

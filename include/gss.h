@@ -156,6 +156,64 @@ int gss_kv_commit(const void* k_win, const void* v_win, int64_t win_layer_stride
                   const int32_t* n_rows, int n_add, int32_t* slots, int bs, int W, int n_layers, int Hkv, int D,
                   int page, void* workspace, size_t workspace_bytes, gss_stream_t stream);
 
+/* ---------------------------------------------------------------- sampled verify (non-greedy requests) ---------
+ * The serving round for requests that sample (selfspec_fast_commit.py:150-230, selfspec_sampling.py:139-293):
+ * gss_penalize_rows gives every verify row the logits processing AR decode gives the same prefix, gss_sample_rows
+ * draws a0 from the draft's causal row (sample mode) or runs speculative sampling of the draft chain against AR's
+ * target distribution (verify mode). Logits are fp32 rows: row b * K + r at logits + (b * K + r) * ld_row.
+ *
+ * gss_penalize_rows (penalize_rows, selfspec_sampling.py:139-198, then logit_bias, selfspec_fast_commit.py:190-191),
+ * in place: row r of sequence b sees the cumulated state of the committed tokens plus its in-block tokens
+ * cand[b, 1..r]; the penalizers run in pen->order (the orchestrator's order): repetition (the penalty at those tokens
+ * set to rep_pen[b]; positive logits divided, others multiplied), presence (set, subtracted), frequency (one
+ * freq_pen[b] added per occurrence, subtracted), min_new_tokens (stop_pen[b] added while len_out[b] + r <
+ * min_new[b]); logit_bias[b] (optional) is added last. State arrays are [bs, V] fp32, parameters [bs]. K <= 64.
+ */
+enum gss_penalizer { GSS_PEN_REPETITION = 1, GSS_PEN_PRESENCE = 2, GSS_PEN_FREQUENCY = 3, GSS_PEN_MIN_NEW_TOKENS = 4 };
+
+typedef struct gss_penalties {
+  int n_order;  /* penalizers in order[0..n_order) (gss_penalizer values, each at most once) */
+  int order[4];
+  const float* rep_cum;
+  const float* rep_pen;
+  const float* pres_cum;
+  const float* pres_pen;
+  const float* freq_cum;
+  const float* freq_pen;
+  const int32_t* len_out;
+  const int32_t* min_new;
+  const float* stop_pen;
+  const float* logit_bias; /* or NULL */
+} gss_penalties;
+
+int gss_penalize_rows(float* logits, int64_t ld_row, int bs, int K, int V, const int32_t* cand,
+                      const gss_penalties* pen, gss_stream_t stream);
+
+/* gss_sample_rows: target distribution of every row (verify_target_probs, selfspec_sampling.py:266-286): softmax of
+ * logits / temperature[b] (temperature <= 0: a point mass at the row maximum), then filter 0 (none), 1 (flashinfer's
+ * joint top-k / top-p: token q kept iff #{p > p_q} < top_k[b] and sum{p > p_q} < top_p[b], top_p >= 1 keeping
+ * all; selfspec_sampling.py:230-244) or 2 (the pytorch backend: rank < top_k, mass before <= top_p, p >= max(p) *
+ * min_p[b]; selfspec_sampling.py:253-263; tied values are kept or dropped together except the top-1 cut, which keeps
+ * the lowest index), renormalized; top_k <= 0 means no top-k cut. A draw with uniform u is the smallest token whose
+ * prefix sum (index order) exceeds u * total.
+ * Sample mode (cand NULL): sampled[b, r] = a draw from row (b, r) with uniforms[b * K + r] (a0 from the draft's
+ * causal row: K = 1, ld_row = the stride between the sequences' rows).
+ * Verify mode (cand = [bs, K] verify ids [a0, d_1..d_{K-1}], coins [bs, K] in (0, 1], uniforms [bs]): sgl-kernel
+ * tree_speculative_sampling_target_only on the chain with a point-mass draft and thresholds 1
+ * (selfspec_fast_commit.py:197-230): row j accepts d_{j+1} iff coins[b, j] <= p_j(d_{j+1}); accept_len[b] = the
+ * first rejected row (K-1 when none); the committed targets are d_1..d_acc and then a draw from row acc without
+ * d_{acc+1} (without removal when acc = K-1, the bonus), written to target[b, 0..acc] (rows past acc: that row's
+ * own draw), next_x0[b] and packed[b] = (a0, acc, targets, zeros) as gss_argmax_accept writes them.
+ * sampled[b, j] = row j's draw without its draft token. Workspace (verify mode): gss_sample_workspace_size bytes,
+ * zeroed once. V <= 65536, K <= 64. */
+int gss_sample_workspace_size(int bs, int K, size_t* bytes);
+
+int gss_sample_rows(const float* logits, int64_t ld_row, int bs, int K, int V, int filter, const float* temperature,
+                    const int32_t* top_k, const float* top_p, const float* min_p, const int32_t* cand,
+                    const float* coins, const float* uniforms, int32_t* sampled, int32_t* target,
+                    int32_t* accept_len, int32_t* next_x0, int32_t* packed, void* workspace, size_t workspace_bytes,
+                    gss_stream_t stream);
+
 /* ---------------------------------------------------------------- skinny GEMMs (decode projections) ----------
  * The dense projections of the decoder layer and the LM head (transformers GlmOcrTextAttention q/k/v/o_proj,
  * GlmOcrTextMLP gate_up/down_proj and lm_head, which the reference runs as torch linears through
