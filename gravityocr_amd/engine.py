@@ -128,17 +128,21 @@ class GssEngine:
     def forward(self, b: _Bufs, *, ids: Optional[torch.Tensor] = None, emb: Optional[torch.Tensor] = None,
                 n_causal: Optional[int], seq_lens: Optional[torch.Tensor] = None,
                 page_table: Optional[torch.Tensor] = None, pos_delta: Optional[torch.Tensor] = None,
-                max_kv_len: Optional[int] = None) -> torch.Tensor:
+                max_kv_len: Optional[int] = None, logits_f32: bool = False) -> torch.Tensor:
         """One window forward of all layers. ``ids`` int32/int64 [bs, W] or ``emb`` [bs*W, H]; n_causal None =
-        verify mask. The window's K/V is left in b.k_win / b.v_win (not committed). Returns logits [bs, W, V]."""
+        verify mask. The window's K/V is left in b.k_win / b.v_win (not committed). Returns logits [bs, W, V] (bf16;
+        fp32 with ``logits_f32``: the LM head's sums before their bf16 rounding, for the sampled round)."""
         c = self.cfg
         bs, W = b.bs, b.W
+        b.want_f32 = logits_f32
         sl = self.seq_lens[:bs] if seq_lens is None else seq_lens
         pt = self.page_table[:bs] if page_table is None else page_table
         mkl = self.max_len if max_kv_len is None else max_kv_len
         own = self.gemm_impl == "gss" and bs * W <= 64
         # the GEMM-prologue norm path (off by default: it would not match the split-K epilogue path bit for bit)
         fused = own and bs * W <= self.fuse_norm_rows and c.hidden % 512 == 0 and c.hidden <= 1536
+        if logits_f32 and (not own or fused):
+            raise NotImplementedError("fp32 logits are produced by the decode GEMM path (bs * W <= 64, unfused norms)")
         if emb is None and ids.dtype == torch.int32 and ids.is_contiguous() and not fused:
             K.embed_rmsnorm(self.embed, ids, self.n_in[0], b.h, b.x, c.rms_eps)   # lookup + first input norm
         else:
@@ -213,6 +217,11 @@ class GssEngine:
                     K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
                 K.gemm(b.act, self.wdown[l], b.a, workspace=ws)
                 K.add_rmsnorm(b.a, self.n_pm[l], h, nxt, b.x, c.rms_eps)
+        if getattr(b, "want_f32", False):
+            if getattr(b, "logits32", None) is None:
+                b.logits32 = torch.empty(bs * W, c.vocab, dtype=torch.float32, device=self.device)
+            K.gemm(b.x, self.lm_head, b.logits32, workspace=ws)
+            return b.logits32.view(bs, W, c.vocab)
         K.gemm(b.x, self.lm_head, b.logits, workspace=ws)
         return b.logits.view(bs, W, c.vocab)
 
