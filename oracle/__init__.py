@@ -21,4 +21,8 @@ Pinning (what each function is checked against, in ``tests/``):
   block diffusion     golden ids / commit traces / commit details written by importing the reference's
                       generate_cached and generate_cached_batched (tests/golden/make_golden_diffusion.py); the
                       unmask rule against a brute-force fp64 reading (tests/test_oracle_diffusion.py)
+  sampled verify      top-k / top-p / min-p filters against their definitions by brute force (ties included); the
+                      in-block penalties against AR decode simulated token by token; speculative sampling against
+                      the identity P(first committed token = t) = p_0(t) over a coin x uniform grid
+                      (tests/test_oracle_sampling.py)
 """
