@@ -1,0 +1,127 @@
+"""The SGLang backend shim (gravityocr_amd/sglang_shim.py) on duck-typed server objects at page size 16:
+  * set_kv_buffer writes each token's K/V to its slot in the kernels' page layout (read back exactly);
+  * forward_extend for both roles equals the oracle's masked attention over the request's committed prefix (read
+    through req_to_token's page-aligned slots) plus the window, within the attention tolerance (1e-2 * max |ref|);
+  * commit equals the oracle's _ss_commit restatement and host loop: next seeds, committed tokens and j, seq_lens
+    (device and host), and the freed rejected verify slots."""
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention import paged_window_attention
+from oracle.integer import host_commit_loop, ss_commit as o_ss_commit
+from tests.test_oracle_integer import _Req
+
+pytestmark = pytest.mark.gpu
+
+
+class _NS:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def _server(cuda, g, lens, K, Hkv=2, D=128, n_layers=2, ctx=2048):
+    """a request pool at page size 16: whole pages handed out from a shuffled free list."""
+    from gravityocr_amd.sglang_shim import PagedKVPool
+    n_pages = sum((L + K + 15) // 16 + 1 for L in lens) + 4
+    pool = PagedKVPool(n_layers, n_pages, Hkv, D, cuda)
+    free = list(g.permutation(n_pages))
+    r2t = torch.zeros(len(lens) + 2, ctx, dtype=torch.int32)
+    for r, L in enumerate(lens):
+        for blk in range((L + K + 15) // 16):
+            pg = int(free.pop())
+            r2t[r + 1, blk * 16:(blk + 1) * 16] = torch.arange(pg * 16, pg * 16 + 16, dtype=torch.int32)
+    return pool, r2t.to(cuda)
+
+
+@pytest.mark.parametrize("role", ["draft", "verify"])
+def test_attention_backend_matches_oracle(cuda, role):
+    from gravityocr_amd.sglang_shim import GssSelfSpecAttnBackend
+    print(f"shim attention {role}", flush=True)
+    g = np.random.default_rng(11 if role == "draft" else 12)
+    lens, K, Hq, Hkv, D = [100, 1000, 37], 17, 16, 2, 128
+    bs = len(lens)
+    pool, r2t = _server(cuda, g, lens, K)
+    rpi = torch.arange(1, bs + 1, dtype=torch.int64, device=cuda)
+    layer = _NS(layer_id=1, scaling=D ** -0.5)
+    # the committed prefixes: every position's K/V written through set_kv_buffer
+    for r, L in enumerate(lens):
+        loc = r2t[r + 1, :L].to(torch.int64)
+        k = (torch.randn(L, Hkv, D, device=cuda) / D ** 0.5).bfloat16()
+        v = (torch.randn(L, Hkv, D, device=cuda) / D ** 0.5).bfloat16()
+        pool.set_kv_buffer(layer.layer_id, loc, k, v)
+        pg, off = loc // 16, loc % 16
+        assert torch.equal(pool.k[1][pg, :, off, :], k) and torch.equal(pool.v[1][pg, :, :, off], v)
+    be = GssSelfSpecAttnBackend(pool, r2t, Hq, Hkv, D, max_bs=4, K=K, max_kv_len=1536)
+    seq_lens = torch.tensor(lens, dtype=torch.int64, device=cuda)
+    out_loc = torch.cat([r2t[r + 1, L:L + K] for r, L in enumerate(lens)]).to(torch.int64)
+    fb = _NS(spec_info=_NS(selfspec_role=role, draft_token_num=K), req_pool_indices=rpi, seq_lens=seq_lens,
+             out_cache_loc=out_loc)
+    q = (torch.randn(bs * K, Hq * D, device=cuda) / D ** 0.5).bfloat16()
+    k = (torch.randn(bs * K, Hkv * D, device=cuda) / D ** 0.5).bfloat16()
+    v = (torch.randn(bs * K, Hkv * D, device=cuda) / D ** 0.5).bfloat16()
+    be.init_forward_metadata(fb)
+    o = be.forward_extend(q, k, v, layer, fb)
+    torch.cuda.synchronize()
+    # the window's K/V landed in its slots too
+    pg, off = out_loc // 16, out_loc % 16
+    assert torch.equal(pool.k[1][pg, :, off, :], k.view(-1, Hkv, D))
+    kp, vp = pool.k[1].cpu(), pool.v[1].cpu()
+    for r, L in enumerate(lens):
+        pt_row = (r2t[r + 1, ::16] // 16).cpu().numpy()
+        ref = paged_window_attention(q.view(bs, K, Hq, D)[r].cpu(), kp, vp, pt_row, L, k.view(bs, K, Hkv, D)[r].cpu(),
+                                     v.view(bs, K, Hkv, D)[r].cpu(), 1 if role == "draft" else K, D ** -0.5)
+        got = o.view(bs, K, Hq, D)[r].float().cpu()
+        err = float((got.double() - ref).abs().max())
+        assert err <= 1e-2 * float(ref.abs().max()), (r, err)
+
+
+class _Alloc:
+    def __init__(self):
+        self.freed = []
+        self.is_not_in_free_group = True
+
+    def free(self, t):
+        self.freed.append(t.clone())
+
+
+@pytest.mark.parametrize("bs,finish", [(1, False), (4, False), (4, True)])
+def test_fast_commit_matches_oracle(cuda, bs, finish):
+    from gravityocr_amd.sglang_shim import GssFastCommit
+    print(f"shim commit bs={bs} finish={finish}", flush=True)
+    g = np.random.default_rng(bs * 3 + finish)
+    K, vocab, pool_n = 5, 10, 8
+    acc = g.integers(0, K, bs).astype(np.int32)
+    predict = g.integers(0, 12, bs * K + 1).astype(np.int32)
+    a0 = g.integers(0, 12, bs).astype(np.int64)
+    rpi = g.permutation(pool_n)[:bs].astype(np.int64)
+    seeds = g.integers(0, 100, pool_n).astype(np.int64)
+    sl = g.integers(10, 50, bs).astype(np.int64)
+    loc = g.permutation(200)[: bs * K].astype(np.int64)
+    budgets = [int(x) for x in g.integers(1, 3 if finish else 40, bs)]
+    reqs = [_Req(bdg, vocab) for bdg in budgets]
+    dev = lambda a: torch.as_tensor(a).to(cuda)
+    vi = _NS(predict=dev(predict), accept_length=dev(acc), a0=dev(a0), draft_token_num=K)
+    seeds_d, sl_d = dev(seeds), dev(sl)
+    batch = _NS(batch_size=lambda: bs, out_cache_loc=dev(loc), req_pool_indices=dev(rpi), seq_lens=sl_d,
+                seq_lens_cpu=torch.as_tensor(sl.copy()), seq_lens_sum=int(sl.sum()), reqs=reqs,
+                token_to_kv_pool_allocator=_Alloc())
+    for r in reqs:
+        r.kv_committed_len = r.kv_allocated_len = 0
+    fc = GssFastCommit(K, 8, cuda)
+    out, toks, js = fc.commit(vi, batch, seeds_d)
+    torch.cuda.synchronize()
+    packed, seeds_w, sl_w, free_w, out_w = o_ss_commit(predict, acc, a0, rpi, seeds.copy(), sl.copy(), loc, K)
+    otoks, ojs, oaccs = host_commit_loop(packed.tolist(), budgets, [{3, 7}] * bs, vocab)
+    assert out.cpu().numpy().tolist() == out_w.tolist()
+    assert np.array_equal(seeds_d.cpu().numpy(), seeds_w)
+    assert toks == otoks and js == ojs
+    want_sl = sl + np.array(js)                    # device lengths after the finished-row fix
+    assert np.array_equal(sl_d.cpu().numpy(), want_sl) and np.array_equal(batch.seq_lens_cpu.numpy(), want_sl)
+    freed = torch.cat(batch.token_to_kv_pool_allocator.freed).cpu().numpy().tolist() if \
+        batch.token_to_kv_pool_allocator.freed else []
+    want_free = [int(s) for i in range(bs) for s in loc[i * K + js[i]:(i + 1) * K]]
+    if bs == 1 or any(j < a + 1 for j, a in zip(js, acc)):
+        assert freed == want_free
+    else:
+        assert freed == free_w.tolist() == want_free
