@@ -325,6 +325,35 @@ def main():
                    "note": "timing includes one host readback per round (loop control)"}
         log(f"planted: {planted}")
 
+    # ---- sampled round (temperature 0.8, top-k 40, top-p 0.9, repetition penalty 1.1), graph-replayed -----------
+    sampled = None
+    if not args.profile_only:
+        from gravityocr_amd.sampling import SampledSelfSpec, SamplingSpec
+        torch.manual_seed(5)
+        ss = SampledSelfSpec(dec, SamplingSpec(temperature=0.8, top_k=40, top_p=0.9, filter="joint",
+                                                repetition_penalty=1.1))
+        eng.seq_lens[:1].fill_(P)
+        ss.start(x00)
+        ss.round()
+        gs = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gs):
+            ss.round()
+        eng.seq_lens[:1].fill_(P)
+        ss.start(x00)
+        n_s = 64
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n_s):
+            gs.replay()
+        torch.cuda.synchronize()
+        sdt = time.perf_counter() - t0
+        saccs = dec.accept_lengths(n_s)[:, 0]
+        sampled = {"us_per_round": round(sdt / n_s * 1e6, 1), "rounds": n_s,
+                   "tokens_per_s": round(int((saccs + 2).sum()) / sdt, 1),
+                   "mean_committed_per_round": round(float((saccs + 2).mean()), 3),
+                   "settings": "temperature 0.8, top-k 40, top-p 0.9 (joint), repetition penalty 1.1"}
+        log(f"sampled: {sampled}")
+
     # ---- draft attention roofline at the round's shape -----------------------------------------------------------
     L = P + args.tokens // 2
     d_us = attn_roofline(dev, L, Kw, eng.max_len)
@@ -386,6 +415,7 @@ def main():
         "speedup_vs_ar": None if ar_tps is None else round(tps / ar_tps, 3),
         "spec_equals_ar_prefix": match,
         "planted": planted,
+        "sampled": sampled,
         "round_hbm_frac": round(round_bytes / (round_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "prefill_s": round(prefill_s, 2),
         "roofline": {"bound": "hbm", "kernel": "gss_draft_attn (block-diffusion draft attention)",

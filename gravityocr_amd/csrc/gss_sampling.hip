@@ -44,7 +44,10 @@ __global__ void __launch_bounds__(PEN_THREADS) penalize_kernel(PenParams p) {
   __shared__ int blk[MAX_K];
   if (threadIdx.x < r) blk[threadIdx.x] = p.cand[static_cast<int64_t>(b) * p.K + 1 + threadIdx.x];
   __syncthreads();
-  const bool min_new_on = p.len_out != nullptr && p.len_out[b] + r < p.min_new[b];
+  // the output-length test only when min_new_tokens is one of the penalizers (then both arrays were checked)
+  bool uses_min_new = false;
+  for (int o = 0; o < p.n_order; ++o) uses_min_new |= p.order[o] == PEN_MIN_NEW_TOKENS;
+  const bool min_new_on = uses_min_new && p.len_out[b] + r < p.min_new[b];
   float* lr = p.logits + static_cast<int64_t>(row) * p.ld_row;
   const int64_t sv = static_cast<int64_t>(b) * p.V;
   const int v0 = blockIdx.x * PEN_THREADS * PEN_PER_THREAD + threadIdx.x;

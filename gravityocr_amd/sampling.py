@@ -122,6 +122,8 @@ class SampledSelfSpec:
         set-type penalties write one value per request, frequency adds one equal amount per token)."""
         st = self.state
         tok = tok.to(torch.int64)
+        # a token outside the vocabulary (a draw from a row without probability mass: NaN logits) is not fed
+        valid = valid & (tok >= 0) & (tok < self.dec.eng.cfg.vocab)
         any_ = valid.any(1, keepdim=True)
         first = tok.gather(1, valid.to(torch.int64).argmax(1, keepdim=True))
         idx = torch.where(valid, tok, torch.where(any_, first, torch.zeros_like(first)))

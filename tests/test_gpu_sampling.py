@@ -161,3 +161,21 @@ def test_verify_mode_chain_matches_oracle(cuda, V, case):
             assert int(sampled[b, a]) == tok
         if case[1] > 0 and case[0] != "joint":
             assert n_acc > 0   # the drafts were built to be accepted sometimes
+
+
+@pytest.mark.parametrize("order", [("repetition",), ("presence", "frequency")])
+def test_penalize_rows_without_min_new_tokens(cuda, order):
+    """Penalizers listed without min_new_tokens: the length / stop arrays are absent (null) and never read."""
+    from gravityocr_amd.kernels import penalize_rows
+    g = np.random.default_rng(21)
+    bs, K, V = 2, 5, 4096
+    st = _state_np(g, bs, V)
+    cand = g.integers(0, V, (bs, K)).astype(np.int32)
+    logits = (g.normal(size=(bs * K, V)) * 3).astype(np.float32)
+    st_np = {k: v for k, v in st.items() if k not in ("min_new", "stop_pen", "logit_bias")}
+    want = S.penalize_rows(logits, cand, st_np, order)
+    dst = _to_dev(st_np, cuda)          # len_out present, min_new / stop_pen absent
+    dl = torch.as_tensor(logits).to(cuda)
+    penalize_rows(dl, torch.as_tensor(cand).to(cuda), dst, order)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dl.cpu().numpy(), want)
