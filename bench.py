@@ -156,6 +156,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--profile-only", action="store_true", help="skip AR, planted and CPU legs (for rocprof runs)")
     ap.add_argument("--ar-only", action="store_true", help="only the graph-replayed AR steps (for rocprof runs)")
+    ap.add_argument("--sampled-only", action="store_true", help="only the graph-replayed sampled rounds (for rocprof runs)")
     ap.add_argument("--attn-only", action="store_true",
                     help="only the draft-attention roofline measurement and the copy calibration (for rocprof runs)")
     ap.add_argument("--attn-batched-only", action="store_true",
@@ -225,7 +226,7 @@ def main():
     # ---- AR baseline: args.tokens AR steps, graph-replayed --------------------------------------------------------
     ar_tps = ar_us = None
     ar_tokens = None
-    if not args.profile_only:
+    if not args.profile_only and not args.sampled_only:
         n_ar = args.tokens + Kw + 2
         reset()
         for _ in range(args.warmup):
@@ -327,7 +328,7 @@ def main():
 
     # ---- sampled round (temperature 0.8, top-k 40, top-p 0.9, repetition penalty 1.1), graph-replayed -----------
     sampled = None
-    if not args.profile_only:
+    if args.sampled_only or not args.profile_only:
         from gravityocr_amd.sampling import SampledSelfSpec, SamplingSpec
         torch.manual_seed(5)
         ss = SampledSelfSpec(dec, SamplingSpec(temperature=0.8, top_k=40, top_p=0.9, filter="joint",
@@ -353,6 +354,9 @@ def main():
                    "mean_committed_per_round": round(float((saccs + 2).mean()), 3),
                    "settings": "temperature 0.8, top-k 40, top-p 0.9 (joint), repetition penalty 1.1"}
         log(f"sampled: {sampled}")
+        if args.sampled_only:
+            print(json.dumps(sampled), flush=True)
+            return
 
     # ---- draft attention roofline at the round's shape -----------------------------------------------------------
     L = P + args.tokens // 2

@@ -114,15 +114,19 @@ GSS_DEV float block_sum_f(float v, float* red) {
   return s;
 }
 
+// Two block sums in one exchange (the count, exact below 2^24, and the mass of a threshold test).
 template <int NW>
-GSS_DEV int block_sum_i(int v, int* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+GSS_DEV float2 block_sum2(float a, float c, float2* red) {
+  a = wave_sum(a);
+  c = wave_sum(c);
   __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = float2{a, c};
   __syncthreads();
-  int s = 0;
-  for (int w = 0; w < NW; ++w) s += red[w];
+  float2 s = red[0];
+  for (int w = 1; w < NW; ++w) {
+    s.x += red[w].x;
+    s.y += red[w].y;
+  }
   return s;
 }
 
@@ -201,7 +205,7 @@ __global__ void __launch_bounds__(NTH) sample_rows_kernel(SvParams p) {
   constexpr int NW = NTH / 64;
   const int row = blockIdx.x, b = row / p.K, j = row % p.K, tid = threadIdx.x;
   __shared__ float redf[NW];
-  __shared__ int redi[NW];
+  __shared__ float2 red2[NW];
   __shared__ float scan[NTH];
   __shared__ float pd_s;
   const float* lr = p.logits + static_cast<int64_t>(row) * p.ld_row;
@@ -270,13 +274,13 @@ __global__ void __launch_bounds__(NTH) sample_rows_kernel(SvParams p) {
       while (lo < hi) {
         const uint32_t mid = lo + (hi - lo) / 2;
         const float tau = __uint_as_float(mid);
-        int c = 0;
-        float ms = 0.f;
+        float c = 0.f, ms = 0.f;
 #pragma unroll
         for (int e = 0; e < EPT; ++e)
-          if (pr[e] > tau) { ++c; ms += pr[e]; }
-        const int C = block_sum_i<NW>(c, redi);
-        const float MS = block_sum_f<NW>(ms, redf);
+          if (pr[e] > tau) { c += 1.f; ms += pr[e]; }
+        const float2 cm = block_sum2<NW>(c, ms, red2);
+        const int C = static_cast<int>(cm.x);
+        const float MS = cm.y;
         const bool ok = p.mode == FILTER_JOINT ? (C < k && (MS < tp || tp >= 1.f)) : (C < k && !(MS > tp));
         if (ok) hi = mid; else lo = mid + 1;
       }
