@@ -7,10 +7,10 @@
 //     share every K/V byte read (row n = w*G + g); rows are MFMA N-tiles of 16. One workgroup takes a unit
 //     (sequence, kv head, key split) for all its rows (up to 10 N-tiles; wider windows use several row groups), so
 //     each K/V byte of the split enters the CU's LDS once.
-//   * Waves are (row wave, key lane) pairs, at most 4, one per SIMD: a row wave owns NGW <= 5 N-tiles (Q fragments
-//     in registers, the O and S accumulators in AGPRs), key lane kl
-//     takes the split's tiles j with j % 2 == kl, whole (64 keys). Each wave runs its own online softmax, so no data
-//     moves between waves until the end, where the two key lanes of a row wave combine in lane order (fp32).
+//   * Waves are (row wave, key lane) pairs, up to 4 x 2: a row wave owns NGW <= 3 N-tiles (Q fragments in
+//     registers), key lane kl takes key half kl (32 keys) of every tile of the split. Each wave runs its own online
+//     softmax, so no data moves between waves until the end, where the two key lanes of a row wave combine in lane
+//     order (fp32).
 //   * Transposed contractions on v_mfma_f32_16x16x32_bf16:  S^T = K Q^T  (M = tokens, N = rows, K = head dim) and
 //     O^T = V^T P^T  (M = head dim, N = rows, K = tokens). A lane then owns one query row per N-tile, so the online
 //     softmax max is two xor-shuffles and the row sum stays lane-local until the end. The P^T operand is the lane's
@@ -18,10 +18,13 @@
 //     moves between lanes.
 //   * K tiles live in LDS as [token][D] with an XOR swizzle of the 16-byte chunks (conflict-free 16-row reads);
 //     V pages are stored token-minor ([D][16] per page) in HBM, so the V^T operand is two 8-byte LDS reads.
-//   * Stages of 2 tiles stream straight from global memory into LDS (global_load_lds_dwordx4; no staging
-//     registers) into two alternating buffers: stage st + 1 is in flight while stage st is computed, with one
-//     workgroup barrier per stage. A stage's page ids are read one stage ahead.
-//   * Grid order is XCD-aware: consecutive units go to different XCDs (ragged batches balance), the row groups of
+//   * Tiles stream straight from global memory into LDS (global_load_lds_dwordx4; no staging registers) through a
+//     ring of 4 one-tile slots: tiles i + 1 .. i + 3 are in flight while tile i is computed, one workgroup barrier
+//     per tile, and each wave waits for exactly its own loads of tile i (vmcnt counts in issue order). The loads
+//     are issued from inline assembly so the compiler does not add a wait for every in-flight LDS load before each
+//     LDS read, which would serialize the ring. The split's page ids are read once into LDS.
+//   * Grid order is XCD-aware: the grid enumerates only the units that hold keys (each workgroup finds its unit from
+//     the device-side lengths), consecutive units go to different XCDs (ragged batches balance), the row groups of
 //     one unit to the same XCD (their repeated K/V reads hit its L2).
 //   * Keys are tiled by absolute position (window rows take the positions after the prefix); the split size and
 //     the tile -> split -> key lane assignment depend only on the capacity max_kv_len and on fixed constants, never
@@ -66,15 +69,16 @@ struct AttnParams {
   uint16_t* out;
   uint16_t* ws_o;  // [bs, Hkv, n_split, R, D] bf16: O / l of each split
   float* ws_ml;    // [bs, Hkv, R, n_split, 2]:      (m, l) of each split (log2 domain max, sum)
-  int pt_stride, prefix_extra, W, n_causal, Hq, Hkv, G, R, n_split, RW, TPG, RG, n_units, tps;
+  int bs, pt_stride, prefix_extra, W, n_causal, Hq, Hkv, G, R, n_split, RW, TPG, RG, n_units, tps;
   float scale_log2;
 };
 
 template <int D>
 struct Lds {
   static constexpr int TILE_EL = TILE * D;          // elements of one K (or V) tile
-  static constexpr int STAGE_EL = 2 * KL * TILE_EL;  // a stage buffer: K [KL][TILE][D] swizzled, V [KL][4][D][16]
-  static constexpr int BUF_BYTES = 2 * STAGE_EL * 2;  // two stage buffers (bytes)
+  static constexpr int NSLOT = 4;                   // one-tile slots of the load ring
+  static constexpr int SLOT_EL = 2 * TILE_EL;       // a slot: K [TILE][D] swizzled, then V [4][D][16]
+  static constexpr int BUF_BYTES = NSLOT * SLOT_EL * 2;  // the ring (bytes)
   static constexpr int TOTAL = BUF_BYTES + 4 * MAX_TPS * 4;  // then the split's page ids (4 pages per tile)
   // combine scratch (reuses the stage buffers): per (row wave, key lane >= 1, N-tile) O^T fp32 and (m, l) of 16 rows
   static constexpr int SCR_FLOATS = (D / 16) * 256 + 32;
@@ -118,13 +122,23 @@ GSS_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
 // resolution of the bf16 probabilities and the fp32 row sums they feed.
 GSS_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Direct global -> LDS load of 16 bytes per lane (global_load_lds_dwordx4: lane i writes its 16 bytes at LDS address
+// `lds` + 16 i; `lds` is wave-uniform and goes through M0). Written as inline assembly so that the compiler does not
+// see an LDS store in flight: it would otherwise wait for every outstanding one (vmcnt(0)) before the next LDS read,
+// including the loads of a stage being prefetched while the current one is computed. The kernels order these loads
+// themselves: s_waitcnt vmcnt on the issuing wave, then a workgroup barrier, before any wave reads the data.
+GSS_DEV void dma16(const void* g, const void* lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
+}
+
 // Boundary tiles ts..te-1 of a stage held in LDS (tile t's K at lds_k + (t - ts) * TILE * D, V likewise), t0 the
 // first tile that reaches past the prefix L: window row j < W (position L + j) comes from k_win / v_win, positions
 // past L + W are zero, and the V chunk that straddles L keeps only its prefix tokens. The thread's first window
 // loads are issued before the LDS pass that clears everything past the prefix, so the whole fix costs about one
 // memory round trip; a workgroup barrier separates the clearing from the window writes, and the caller follows
 // with another before the tiles are read.
-template <int D>
+template <int D, bool RETIRE = false>
 GSS_DEV void fix_boundary(uint16_t* lds_k, uint16_t* lds_v, int ts, int t0, int te, int L, int W,
                           const uint16_t* k_win, const uint16_t* v_win, int64_t win_base, int Hkv, int tid,
                           int nthr) {
@@ -177,6 +191,11 @@ GSS_DEV void fix_boundary(uint16_t* lds_k, uint16_t* lds_v, int ts, int t0, int 
           static_cast<uint16_t>((e & 1) ? (vw[e >> 1] >> 16) : (vw[e >> 1] & 0xffffu));
     }
   }
+  // RETIRE (callers that keep loads of their own in flight across this call): the window loads of lanes past n_win
+  // were never consumed; retire them here (a wait the compiler accounts for), so no load the compiler tracks is
+  // pending when the caller's loop continues (it would otherwise wait for every vector memory operation before
+  // reusing their registers, prefetched tiles included)
+  if (RETIRE) __builtin_amdgcn_s_waitcnt(0);
 }
 
 GSS_DEV int valid_splits(int L, int W, int tps) {
@@ -192,21 +211,61 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   constexpr int CH = D / 8;    // 16-byte chunks per K row
   constexpr int TILE_EL = Lds<D>::TILE_EL;
   constexpr int TILE_INSTR = TILE * CH / 64;    // direct-load instructions per K (or V) tile
-  constexpr int STAGE_INSTR = 2 * KL * TILE_INSTR;  // K and V of the KL tiles of a stage
   constexpr int PAGE_INSTR = PAGE * CH / 64;    // instructions per (page, head) block of K (or V)
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
 
-  // Grid order: workgroups are dealt to the 8 XCDs round-robin by linear index. A unit u = (sequence, kv head,
-  // split), numbered split-fastest, runs as workgroups (u / 8) * 8 * RG + rg * 8 + u % 8 for its RG row groups: all
-  // of them on XCD u % 8, dispatched back to back (so they share that XCD's L2 for the unit's K/V), and consecutive
-  // units (the splits of one sequence) on different XCDs, so ragged sequences, whose late splits are empty, spread
-  // their work evenly over the XCDs.
+  // Grid order: workgroups are dealt to the 8 XCDs round-robin by linear index. The grid enumerates only the units
+  // (sequence, kv head, split) that hold keys: unit v of that list (sequence-major, split fastest) runs as workgroups
+  // (v / 8) * 8 * RG + rg * 8 + v % 8 for its RG row groups, all of them on XCD v % 8, dispatched back to back (so
+  // they share that XCD's L2 for the unit's K/V), and consecutive units on different XCDs. Ragged sequences (whose
+  // late splits are empty) thus spread their work evenly over the XCDs; numbering all units instead would put
+  // split s of every sequence on XCD s % 8. Each workgroup finds its unit from the device-side lengths (wave 0 scans
+  // the valid split counts of the batch), so the host needs no length and the launch stays graph-capturable.
   const int r8 = blockIdx.x % (8 * p.RG);
-  const int u = blockIdx.x / (8 * p.RG) * 8 + r8 % 8, rg = r8 / 8;
-  if (u >= p.n_units) return;  // padding of the last group of 8 units
-  const int s = u % p.n_split, kvh = (u / p.n_split) % p.Hkv, b = u / (p.n_split * p.Hkv);
+  const int v = blockIdx.x / (8 * p.RG) * 8 + r8 % 8, rg = r8 / 8;
+  if (v >= p.n_units) return;  // padding of the last group of 8 units
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __shared__ int s_unit[3];  // (sequence, kv head, split) of unit v; sequence -1: v is past the valid units
+  if (wv == 0) {
+    int base = 0;  // valid units of the sequences before this 64-sequence chunk
+    int found = -1, fh = 0, fs = 0;
+    for (int c = 0; c < p.bs && found < 0 && base <= v; c += 64) {
+      const int bb = c + lane;
+      int nvb = 0;  // valid splits of sequence bb
+      if (bb < p.bs) {
+        const int Lb = min(max(p.prefix_len[bb] + p.prefix_extra, 0), p.pt_stride * PAGE);
+        nvb = min(p.n_split, valid_splits(Lb, p.W, p.tps));
+      }
+      int inc = nvb * p.Hkv;  // inclusive prefix sum of the chunk's unit counts
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(inc, o, 64);
+        if (lane >= o) inc += t;
+      }
+      const int lo = base + inc - nvb * p.Hkv;
+      const bool mine = bb < p.bs && v >= lo && v < base + inc;
+      const unsigned long long bal = __ballot(mine);
+      if (bal) {
+        const int src = __builtin_ctzll(bal);
+        const int r = __shfl(v - lo, src, 64), nv = __shfl(nvb, src, 64);
+        found = c + src;
+        fh = r / nv;
+        fs = r % nv;
+      }
+      base += __shfl(inc, 63, 64);
+    }
+    if (lane == 0) {
+      s_unit[0] = found;
+      s_unit[1] = fh;
+      s_unit[2] = fs;
+    }
+  }
+  __syncthreads();
+  // workgroup-uniform (readfirstlane keeps them and every address derived from them in scalar registers)
+  const int b = __builtin_amdgcn_readfirstlane(s_unit[0]), kvh = __builtin_amdgcn_readfirstlane(s_unit[1]),
+            s = __builtin_amdgcn_readfirstlane(s_unit[2]);
+  if (b < 0) return;  // past the last valid unit
   const int kl = wv % KL, rw = wv / KL;                       // key lane, row wave
   const int l16 = lane & 15, g4 = lane >> 4;
   // committed prefix length; clamped to what the page-table row can address so every page-table read is in bounds
@@ -218,6 +277,10 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   const int32_t* pt = p.page_table + static_cast<int64_t>(b) * p.pt_stride;
   const int64_t head_stride = static_cast<int64_t>(PAGE) * D;          // elements per (page, kv head) block
   const int64_t win_base = static_cast<int64_t>(b) * W * p.Hkv + kvh;  // window row j: (win_base + j*Hkv)*D
+  // this kv head's block of page 0 in the K and V pools; page pg's block is page_stride elements further
+  const uint16_t* kp_head = p.k_pages + kvh * head_stride;
+  const uint16_t* vp_head = p.v_pages + kvh * head_stride;
+  const int64_t page_stride = p.Hkv * head_stride;
 
   // ---- this wave's query fragments (the B operand of S^T = K Q^T), in registers for the whole kernel: N-tiles
   // nt0 .. nt0 + ng - 1 (ng <= NGW, wave-uniform) of the sequence's R = G*W rows. Rows past R have zero queries and
@@ -260,66 +323,70 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
     }
   __syncthreads();
 
-  // ---- stage loads, global -> LDS directly (global_load_lds_dwordx4: lane i of an instruction writes the 16 bytes
-  // at the instruction's LDS base + 16 i). A stage is KL tiles, held in buffer st % 2 as K [KL][TILE][D] (XOR-swizzled
-  // 16-byte chunks) then V [KL][4 pages][D][16]. Every instruction covers 64 chunks of one (page, head) block, so its
-  // page id is wave-uniform. Chunks of positions >= L are not loaded.
-  auto issue_stage = [&](int st) {
-    uint16_t* buf = smem + (st & 1) * Lds<D>::STAGE_EL;
-    // lane j holds page j of the stage (one LDS read per lane); readlane broadcasts the one an instruction needs
-    const int pgv = lane < KL * (TILE / PAGE) && st * KL * (TILE / PAGE) + lane < (t_end - t_beg) * (TILE / PAGE)
-                        ? spages[st * KL * (TILE / PAGE) + lane]
-                        : 0;
-#pragma unroll 1  // unrolled, the per-instruction lane offsets are hoisted out of the stage loop and spilled
-    for (int i = 0; i < (STAGE_INSTR + NW - 1) / NW; ++i) {
-      const int ii = wv + i * NW;
-      if (ii >= STAGE_INSTR) break;
-      const bool is_v = ii >= KL * TILE_INSTR;
-      const int iv = is_v ? ii - KL * TILE_INSTR : ii;
-      const int tl = iv / TILE_INSTR, ib = iv % TILE_INSTR;
-      const int t = t_beg + st * KL + tl;
-      if (t >= t_end) continue;
+  // ---- tile loads, global -> LDS directly (dma16: lane i of an instruction writes the 16 bytes at the
+  // instruction's LDS base + 16 i) into a ring of NSLOT one-tile slots, each K [TILE][D] (XOR-swizzled 16-byte
+  // chunks) then V [4 pages][D][16]. Every instruction covers 64 chunks of one (page, head) block, so its page id is
+  // wave-uniform. Loads are unconditional: pages past the prefix read page 0 (in bounds) and the boundary fix
+  // overwrites those positions, so every wave issues exactly `per_tile` instructions per tile and the wait for tile
+  // i is an exact count of the loads issued after it.
+  constexpr int NSLOT = Lds<D>::NSLOT;
+  const int per_tile = (2 * TILE_INSTR - wv + NW - 1) / NW;  // this wave's instructions per tile
+  auto issue_tile = [&](int i) {  // tile t_beg + i of the split -> slot i % NSLOT
+    uint16_t* buf = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
+    const int pgv = lane < TILE / PAGE ? spages[i * (TILE / PAGE) + lane] : 0;
+#pragma unroll 1  // unrolled, the per-instruction lane offsets are hoisted out of the tile loop and spilled
+    for (int k = 0; k < (2 * TILE_INSTR + NW - 1) / NW; ++k) {
+      const int ii = wv + k * NW;
+      if (ii >= 2 * TILE_INSTR) break;
+      const bool is_v = ii >= TILE_INSTR;
+      const int ib = is_v ? ii - TILE_INSTR : ii;
       const int pblk = ib / PAGE_INSTR, pat = ib % PAGE_INSTR;
-      const int pos0 = t * TILE + pblk * PAGE;  // first position of the page
       const int kr = pat * 64 + lane;
-      int off, first;  // element offset in the (page, head) block; position of the chunk's first token
+      int off;  // element offset in the (page, head) block
       if (is_v) {
         const int vd = kr >> 1, vh = (kr & 1) ^ ((vd >> 3) & 1);
         off = vd * PAGE + vh * 8;
-        first = pos0 + vh * 8;
       } else {
         const int ktok = kr / CH;
         off = ktok * D + ((kr % CH) ^ (ktok & (CH - 1))) * 8;
-        first = pos0 + ktok;
       }
-      const int64_t page = __builtin_amdgcn_readlane(pgv, tl * (TILE / PAGE) + pblk);
-      const uint16_t* base = (is_v ? p.v_pages : p.k_pages) + (page * p.Hkv + kvh) * head_stride;
-      lvoid_t* dst = (lvoid_t*)(buf + (is_v ? KL * TILE_EL : 0) + iv * 512);
-      if (pos0 + PAGE <= L)  // page wholly inside the prefix (wave-uniform): no per-lane test
-        __builtin_amdgcn_global_load_lds((gvoid_t*)(base + off), dst, 16, 0, 0);
-      else if (first < L)
-        __builtin_amdgcn_global_load_lds((gvoid_t*)(base + off), dst, 16, 0, 0);
+      const int64_t page = __builtin_amdgcn_readlane(pgv, pblk);
+      dma16((is_v ? vp_head : kp_head) + page * page_stride + off, buf + (is_v ? TILE_EL : 0) + ib * 512);
     }
   };
-  // Tiles that reach past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
+  // wait until this wave's loads of the tile `ahead` tiles before the newest one issued have landed (vmcnt counts
+  // in issue order; the count is an immediate, hence the switch)
+  auto wait_tile = [&](int ahead) {
+    switch (ahead * per_tile) {
+#define GSS_VMW(n) \
+  case n:          \
+    asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); \
+    break;
+      GSS_VMW(1) GSS_VMW(2) GSS_VMW(3) GSS_VMW(4) GSS_VMW(5) GSS_VMW(6) GSS_VMW(8) GSS_VMW(10) GSS_VMW(12)
+      GSS_VMW(16) GSS_VMW(24) GSS_VMW(32)
+#undef GSS_VMW
+      default:
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+  };
+  // Tile i reaching past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
   // and the V chunk that straddles L keeps only its prefix tokens.
-  auto fix_stage = [&](int st) {
-    uint16_t* lds_k = smem + (st & 1) * Lds<D>::STAGE_EL;
-    const int ts = t_beg + st * KL, te = min(t_end, ts + KL);
-    const int t0 = max(ts, L / TILE);
-    if (t0 >= te) return false;
-    fix_boundary<D>(lds_k, lds_k + KL * TILE_EL, ts, t0, te, L, W, p.k_win, p.v_win, win_base, p.Hkv, tid,
-                    blockDim.x);
+  auto fix_tile = [&](int i) {
+    const int t = t_beg + i;
+    if ((t + 1) * TILE <= L) return false;
+    uint16_t* lds_k = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
+    fix_boundary<D, true>(lds_k, lds_k + TILE_EL, t, t, t + 1, L, W, p.k_win, p.v_win, win_base, p.Hkv, tid,
+                          blockDim.x);
     return true;
   };
 
-  // ---- online softmax, private to the wave: key lane kl takes tiles t_beg + kl, t_beg + kl + KL, ... of the split,
-  // each whole (4 m-tiles of 16 keys), for its ng N-tiles. Scores come out of the MFMA in the log2 domain (the
-  // queries are pre-scaled). Each row keeps a reference max m that trails its running max by at most RESCALE_SLACK,
-  // and P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more than the slack
-  // (rare after the first tiles) does the wave take the row maxima (two xor-shuffles over the row's lanes), move the
-  // references and rescale O and l. P^T is packed to bf16 in the lane that scored it, and O^T += V^T P^T over
-  // 2 K-steps of 32 keys.
+  // ---- online softmax, private to the wave: key lane kl takes key half kl (32 keys, m-tiles 2 kl and 2 kl + 1)
+  // of every tile of the split, for its ng N-tiles. Scores come out of the MFMA in the log2 domain (the queries are
+  // pre-scaled). Each row keeps a reference max m that trails its running max by at most RESCALE_SLACK, and
+  // P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more than the slack (rare
+  // after the first tiles) does the wave take the row maxima (two xor-shuffles over the row's lanes), move the
+  // references and rescale O and l. P^T is packed to bf16 in the lane that scored it, and O^T += V^T P^T over one
+  // K-step of 32 keys.
   floatx4_t o[NGW][DT];
   float m_run[NGW], l_run[NGW];
 #pragma unroll
@@ -331,40 +398,42 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   }
   const int hsw = (l16 >> 3) & 1;  // the V half swap of head dims d with bit 3 set (d = dt*16 + l16)
   const int vrd = ((g4 >> 1) ^ hsw) * 8 + (g4 & 1) * 4;
+  const int hh = kl;               // this wave's key half of every tile
 
-  const int n_stages = (t_end - t_beg + KL - 1) / KL;
-  issue_stage(0);
-  for (int st = 0; st < n_stages; ++st) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of stage st
-    __syncthreads();  // every wave's loads of stage st have landed; every wave is done with stage st - 1's buffer
-    if (fix_stage(st)) __syncthreads();  // block-uniform condition
-    if (st + 1 < n_stages) issue_stage(st + 1);  // stream stage st + 1 into the other buffer while st is computed
-    const int tb = (t_beg + st * KL + kl) * TILE;
-    if (tb >= t_end * TILE) continue;  // wave-uniform: this key lane has no tile in the last stage
-    const uint16_t* tk = smem + (st & 1) * Lds<D>::STAGE_EL + kl * TILE_EL;
-    const uint16_t* tv = tk + KL * TILE_EL;
-    // the tile in two halves of 32 keys (half hh: m-tiles 2hh and 2hh+1, the P^T slots 0..3 and 4..7 of K-step hh),
-    // each: scores, mask, row maxima and reference moves, P^T, then O^T += V^T P^T. LDS fragments are read one step
+  const int n_t = t_end - t_beg;
+  // nothing the compiler tracks may be outstanding when the tile loop starts: a load or spill store still pending
+  // at the loop header would make it wait for every vector memory operation inside the loop, the prefetched tiles
+  // included (a real s_waitcnt, which the compiler's wait insertion accounts for)
+  __builtin_amdgcn_s_waitcnt(0);
+  for (int i = 0; i < min(NSLOT - 1, n_t); ++i) issue_tile(i);
+  for (int i = 0; i < n_t; ++i) {
+    wait_tile(min(NSLOT - 2, n_t - 1 - i));  // this wave's loads of tile i
+    __syncthreads();  // every wave's loads of tile i have landed; every wave is done with tile i - 1's slot
+    if (fix_tile(i)) __syncthreads();  // block-uniform condition
+    if (i + NSLOT - 1 < n_t) issue_tile(i + NSLOT - 1);  // into the slot of tile i - 1
+    const int tb = (t_beg + i) * TILE;
+    const uint16_t* tk = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
+    const uint16_t* tv = tk + TILE_EL;
+    // scores, mask, row maxima and reference moves, P^T, then O^T += V^T P^T. LDS fragments are read one step
     // ahead of the MFMAs that use them.
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
+    {
       floatx4_t sacc[NGW][2];
 #pragma unroll
       for (int g = 0; g < NGW; ++g) sacc[g][0] = sacc[g][1] = floatx4_t{0.f, 0.f, 0.f, 0.f};
       // K-step outer, m-tile inner: consecutive MFMAs go to 2 * ng different accumulators, so a dependent one
       // (same accumulator, next K-step) is never issued right behind its predecessor
-      auto kfrag = [&](int i) {  // i = ks * 2 + mt over the half's 2 m-tiles
-        return *reinterpret_cast<const bf16x8_t*>(&tk[k_lds_index<D>((2 * hh + (i & 1)) * 16 + l16, (i >> 1) * 4 + g4)]);
+      auto kfrag = [&](int i2) {  // i2 = ks * 2 + mt over the half's 2 m-tiles
+        return *reinterpret_cast<const bf16x8_t*>(&tk[k_lds_index<D>((2 * hh + (i2 & 1)) * 16 + l16, (i2 >> 1) * 4 + g4)]);
       };
       bf16x8_t a_cur = kfrag(0);
 #pragma unroll
-      for (int i = 0; i < 2 * KS; ++i) {
+      for (int i2 = 0; i2 < 2 * KS; ++i2) {
         bf16x8_t a_nxt = a_cur;
-        if (i + 1 < 2 * KS) a_nxt = kfrag(i + 1);
+        if (i2 + 1 < 2 * KS) a_nxt = kfrag(i2 + 1);
 #pragma unroll
         for (int g = 0; g < NGW; ++g)
           if (g < ng)
-            sacc[g][i & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, qf[g][i >> 1], sacc[g][i & 1], 0, 0, 0);
+            sacc[g][i2 & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, qf[g][i2 >> 1], sacc[g][i2 & 1], 0, 0, 0);
         a_cur = a_nxt;
       }
       if (tb + TILE > L) {  // keys past the prefix: the window mask (wave-uniform branch)
@@ -375,11 +444,11 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int pos = tb + (2 * hh + mt) * 16 + g4 * 4 + i;
+            for (int e = 0; e < 4; ++e) {
+              const int pos = tb + (2 * hh + mt) * 16 + g4 * 4 + e;
               const int wj = pos - L;
               const bool vis = pos < L || (wj < W && (roww >= nc || wj <= roww));
-              if (!vis) sacc[g][mt][i] = -INFINITY;
+              if (!vis) sacc[g][mt][e] = -INFINITY;
             }
         }
       }
@@ -777,81 +846,103 @@ __global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams
 }
 
 
-// Combine the valid splits of each (sequence, kv head, row): block = one query row, 256 threads = (D/2 dim pairs) x
-// (SG split groups). All loads are issued in one round: the prefix length, the row's (m, l) of every split (stored
-// contiguously per row; splits past the valid count are masked), and each thread's partial-O pairs. Weights
-// w_s = l_s * 2^(m_s - M) follow from one wave-wide max; thread (dp, sg) sums w_s * O_s over s = sg mod SG with
-// fused multiply-adds in split order, and the SG groups and the weights are reduced in a fixed order. A split that
-// holds none of the row's visible keys has w_s = 0 exactly.
+// Combine the valid splits of each (sequence, kv head, row): one wave (and workgroup) per row. A split's partial
+// row is D bf16 = D/8 chunks of 16 bytes, so the wave reads SGW = 64 / (D/8) split rows per instruction (lane =
+// split group sg x chunk dc) and issues the loads of up to PRE * SGW splits before it waits; the row's (m, l) of every
+// split (stored contiguously per row) are read in the same round, one split per lane. Weights w_s = l_s * 2^(m_s - M)
+// follow from one wave max; lane (sg, dc) sums w_s * O_s over s = sg mod SGW with fused multiply-adds in split order,
+// and the split groups combine by xor-shuffles in a fixed order. Splits past the valid count hold whatever an earlier
+// call left in the workspace and are neither loaded nor weighted. A split that holds none of the row's visible keys
+// has w_s = 0 exactly.
 template <int D>
-__global__ void __launch_bounds__(256) window_attn_merge(AttnParams p) {
-  constexpr int DP = D / 2, SG = 256 / DP, PRE = 16;  // PRE: partial-O loads per thread issued up front
-  const int n = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, dp = tid % DP, sg = tid / DP;
+__global__ void __launch_bounds__(64) window_attn_merge(AttnParams p) {
+  constexpr int CPL = D / 8, SGW = 64 / CPL, PRE = 16, MLR = MAX_SPLIT / 64;
+  static_assert(PRE * SGW <= MAX_SPLIT, "the first round's splits must have weights");
+  const int lane = threadIdx.x & 63;
+  const int64_t rid = blockIdx.x;  // (b * Hkv + kvh) * R + n
+  const int n = static_cast<int>(rid % p.R), bh = static_cast<int>(rid / p.R), kvh = bh % p.Hkv, b = bh / p.Hkv;
+  const int sg = lane / CPL, dc = lane % CPL;
   const int ns = p.n_split;
-  const int64_t rowid = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.R + n;
-  const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + rowid * ns;
-  const uint16_t* obase = p.ws_o + (static_cast<int64_t>(b) * p.Hkv + kvh) * ns * p.R * D +
-                          static_cast<int64_t>(n) * D + 2 * dp;
+  const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + rid * ns;
+  const uint16_t* obase = p.ws_o + static_cast<int64_t>(bh) * ns * p.R * D + static_cast<int64_t>(n) * D + dc * 8;
   const int64_t ostride = static_cast<int64_t>(p.R) * D;
-  __shared__ float sw[MAX_SPLIT];
-  __shared__ float red[4];
-  __shared__ float2 sacc[SG][DP];
-  // every independent load in one round: prefix length, (m, l) of split tid, this thread's first PRE O pairs
+  // one round of loads: the length, and (m, l) and the first PRE * SGW partial rows of every split of the workspace
+  // (in bounds whatever the length); the valid count masks them afterwards
   const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.pt_stride * PAGE);
-  const float2 mlv = tid < ns ? ml[tid] : float2{-INFINITY, 0.f};
-  uint32_t u[PRE];
+  float2 mlv[MLR];
+#pragma unroll
+  for (int k = 0; k < MLR; ++k) {
+    const int sp = lane + 64 * k;
+    mlv[k] = sp < ns ? ml[sp] : float2{-INFINITY, 0.f};
+  }
+  u32x4_t u[PRE];
 #pragma unroll
   for (int k = 0; k < PRE; ++k) {
-    const int s = sg + k * SG;
-    u[k] = s < ns ? *reinterpret_cast<const uint32_t*>(obase + s * ostride) : 0u;
+    const int sp = sg + k * SGW;
+    u[k] = sp < ns ? *reinterpret_cast<const u32x4_t*>(obase + sp * ostride) : u32x4_t{0u, 0u, 0u, 0u};
   }
   const int nv = min(ns, valid_splits(L, p.W, p.tps));
-  float mloc = wave_max(tid < nv ? mlv.x : -INFINITY);
-  if ((tid & 63) == 0) red[tid >> 6] = mloc;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float Mu = M == -INFINITY ? 0.f : M;
-  sw[tid] = tid < nv ? mlv.y * exp2f(mlv.x - Mu) : 0.f;
-  __syncthreads();
-  float ax = 0.f, ay = 0.f;
+  float mx = lane < nv ? mlv[0].x : -INFINITY;
 #pragma unroll
-  for (int k = 0; k < PRE; ++k) {  // splits sg, sg + SG, ... in order, with fused multiply-adds
-    const int s = sg + k * SG;
-    // splits past the valid count hold whatever an earlier call left in the workspace: drop the value, not just
-    // its weight (0 * inf would be NaN)
-    const float w = s < nv ? sw[s] : 0.f;
-    const uint32_t v = s < nv ? u[k] : 0u;
-    ax = __builtin_fmaf(w, __uint_as_float(v << 16), ax);
-    ay = __builtin_fmaf(w, __uint_as_float(v & 0xffff0000u), ay);
-  }
-  for (int s = sg + PRE * SG; s < nv; s += SG) {  // more than PRE * SG splits: the rest, in the same order
-    const uint32_t v = *reinterpret_cast<const uint32_t*>(obase + s * ostride);
-    const float w = sw[s];
-    ax = __builtin_fmaf(w, __uint_as_float(v << 16), ax);
-    ay = __builtin_fmaf(w, __uint_as_float(v & 0xffff0000u), ay);
-  }
-  sacc[sg][dp] = float2{ax, ay};
-  __syncthreads();
-  if (sg != 0) return;
+  for (int k = 1; k < MLR; ++k) mx = fmaxf(mx, lane + 64 * k < nv ? mlv[k].x : -INFINITY);
+  const float M = wave_max(mx);
+  const float Mu = M == -INFINITY ? 0.f : M;
+  float wk[MLR];  // weight of split lane + 64 k (0 past the valid count)
   float den = 0.f;
-  for (int k = 0; k < nv; ++k) den += sw[k];
-  for (int g = 1; g < SG; ++g) {
-    ax += sacc[g][dp].x;
-    ay += sacc[g][dp].y;
+#pragma unroll
+  for (int k = 0; k < MLR; ++k) {
+    wk[k] = lane + 64 * k < nv ? mlv[k].y * exp2f(mlv[k].x - Mu) : 0.f;
+    den += wk[k];
   }
+  den = wave_sum(den);
+  auto weight = [&](int sp) {  // w of split sp (< MAX_SPLIT), from lane sp % 64
+    float w = 0.f;
+#pragma unroll
+    for (int k = 0; k < MLR; ++k) {
+      const float t = __shfl(wk[k], sp & 63, 64);
+      if ((sp >> 6) == k) w = t;
+    }
+    return w;
+  };
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  auto fma_row = [&](float w, const u32x4_t& x) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[2 * e] = __builtin_fmaf(w, __uint_as_float(x[e] << 16), acc[2 * e]);
+      acc[2 * e + 1] = __builtin_fmaf(w, __uint_as_float(x[e] & 0xffff0000u), acc[2 * e + 1]);
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < PRE; ++k) {  // split sg + k SGW: its weight sits in register (k SGW) / 64 of lane (sp % 64)
+    const int sp = sg + k * SGW;
+    const float w = __shfl(wk[(k * SGW) >> 6], sp & 63, 64);
+    if (sp < nv) fma_row(w, u[k]);
+  }
+  for (int sp0 = PRE * SGW; sp0 < nv; sp0 += SGW) {  // more than PRE * SGW splits: the rest, in the same order
+    const int sp = sp0 + sg;
+    const float w = weight(sp < MAX_SPLIT ? sp : 0);
+    if (sp < nv) fma_row(w, *reinterpret_cast<const u32x4_t*>(obase + sp * ostride));
+  }
+#pragma unroll
+  for (int o = CPL; o < 64; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  if (sg != 0) return;
   const float inv = den > 0.f ? 1.f / den : 0.f;
-  const int w = n / p.G, gq = n % p.G;
-  uint16_t* orow = p.out + ((static_cast<int64_t>(b) * p.W + w) * p.Hq + kvh * p.G + gq) * D;
-  *reinterpret_cast<uint32_t*>(orow + 2 * dp) = cvt_pk_bf16(ax * inv, ay * inv);
+  uint16_t* orow = p.out + ((static_cast<int64_t>(b) * p.W + n / p.G) * p.Hq + kvh * p.G + n % p.G) * D + dc * 8;
+  *reinterpret_cast<u32x4_t*>(orow) = u32x4_t{cvt_pk_bf16(acc[0] * inv, acc[1] * inv), cvt_pk_bf16(acc[2] * inv, acc[3] * inv),
+                                             cvt_pk_bf16(acc[4] * inv, acc[5] * inv), cvt_pk_bf16(acc[6] * inv, acc[7] * inv)};
 }
 
 // Split sizing: tiles per split from the capacity (max_kv_len plus a full window) and bs * Hkv only, so every call
 // on the same cache and batch size partitions the keys identically: about target_wgs / (bs * Hkv) splits per
 // sequence and kv head, each at least min_tiles tiles (gss_attn_set_split_policy). At bs = 1 the minimum decides
 // (short splits fill the chip); a large batch gets few long splits, which keeps the partial traffic and the merge
-// small (32 ragged sequences of up to 12K keys: 8 splits of 25 tiles, 1.8x faster than 4 splits of 49).
-int g_target_wgs = 512, g_min_tiles = 4;
+// small (32 ragged sequences of up to 12K keys with a 17-row window: 12 splits of 17 tiles, 93 us per call, against
+// 122 us for 8 of 25 and 109 us for 15 of 13).
+int g_target_wgs = 768, g_min_tiles = 4;
 int g_wide_min = 16;  // batches with bs * Hkv >= this run the wide kernel (gss_attn_set_wide_min)
 
 int attn_plan(int bs, int Hkv, int max_kv_len, int* n_split, int* tps) {
@@ -929,7 +1020,8 @@ int launch_d(const AttnParams& p, int bs, bool wide, int ng, hipStream_t st) {
     else
       hipLaunchKernelGGL((attn_rowgroup_kernel<D, 3>), grid, dim3(RG_THREADS), lds, st, p);
   }
-  if (p.n_split > 1) hipLaunchKernelGGL((window_attn_merge<D>), dim3(p.R, p.Hkv, bs), dim3(256), 0, st, p);
+  if (p.n_split > 1)
+    hipLaunchKernelGGL((window_attn_merge<D>), dim3(bs * p.Hkv * p.R), dim3(64), 0, st, p);
   return gss_launch_status();
 }
 
@@ -964,6 +1056,7 @@ int attn_entry(const void* q, const void* k_pages, const void* v_pages, const in
   p.R = p.G * W;
   rc = attn_plan(bs, Hkv, max_kv_len, &p.n_split, &p.tps);
   if (rc != GSS_OK) return rc;
+  p.bs = bs;
   p.n_units = bs * Hkv * p.n_split;
   // kernel: a function of the batch shape only (never of W), so every window size of one batch runs the same one
   const bool wide = bs * Hkv >= g_wide_min;
