@@ -170,25 +170,31 @@ __global__ void __launch_bounds__(64 * NORM_ROWS_PER_BLOCK) add_rmsnorm_kernel(c
   store_row<E>(x + off, av);
 }
 
-// The same with a given as n_parts fp32 partial sums [n_parts][rows][H] (a skinny GEMM's k splits): a = bf16 of
-// their sum, added in part order. One wavefront per row, one row per workgroup (the parts are the bulk of the reads).
-template <int E>
-__global__ void __launch_bounds__(64) add_rmsnorm_parts_kernel(const float* parts, int n_parts,
-                                                               const uint16_t* w_post, uint16_t* h,
-                                                               const uint16_t* w_next, uint16_t* x, int rows,
-                                                               float eps) {
+// The same with a given as NP fp32 partial sums [NP][rows][H] (a skinny GEMM's k splits): a = bf16 of their sum,
+// added in part order. One wavefront per row, one row per workgroup (the parts are the bulk of the reads). NP is a
+// compile-time count so every part load of the row is issued before the first one is used: one memory round trip.
+template <int E, int NP>
+__global__ void __launch_bounds__(64) add_rmsnorm_parts_kernel(const float* parts, const uint16_t* w_post,
+                                                               uint16_t* h, const uint16_t* w_next, uint16_t* x,
+                                                               int rows, float eps) {
   constexpr int H = 64 * E;
   const int row = blockIdx.x, lane = threadIdx.x;
   const int64_t off = static_cast<int64_t>(row) * H + lane * E;
   float av[E], hv[E], wp[E], wn[E];
+  const int64_t pstride = static_cast<int64_t>(rows) * H;
+  floatx4_t pv[NP][E / 4];
+#pragma unroll
+  for (int k = 0; k < NP; ++k)
+#pragma unroll
+    for (int e = 0; e < E; e += 4) pv[k][e / 4] = *reinterpret_cast<const floatx4_t*>(parts + k * pstride + off + e);
   load_row<E>(h + off, hv);
   load_row<E>(w_post + lane * E, wp);
   load_row<E>(w_next + lane * E, wn);
-  const int64_t pstride = static_cast<int64_t>(rows) * H;
 #pragma unroll
   for (int e = 0; e < E; e += 4) {
-    floatx4_t s = *reinterpret_cast<const floatx4_t*>(parts + off + e);
-    for (int k = 1; k < n_parts; ++k) s += *reinterpret_cast<const floatx4_t*>(parts + k * pstride + off + e);
+    floatx4_t s = pv[0][e / 4];
+#pragma unroll
+    for (int k = 1; k < NP; ++k) s += pv[k][e / 4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) av[e + i] = round_bf16(s[i]);
   }
@@ -312,18 +318,23 @@ extern "C" int gss_add_rmsnorm_parts(const float* parts, int n_parts, const void
                                      void* x, int rows, int H, float eps, gss_stream_t stream) {
   if (!parts || !w_post || !h || !w_next || !x || rows <= 0 || H <= 0 || n_parts < 1) return GSS_ERR_ARG;
   if (reinterpret_cast<uintptr_t>(parts) & 15u) return GSS_ERR_ARG;
-  if (H % 64 != 0 || H / 64 > MAX_E || (H / 64) % 4 != 0) return GSS_ERR_UNSUPPORTED;
+  if (H % 64 != 0 || H / 64 > MAX_E || (H / 64) % 4 != 0 || n_parts > 4) return GSS_ERR_UNSUPPORTED;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t *wp = static_cast<const uint16_t*>(w_post), *wn = static_cast<const uint16_t*>(w_next);
   uint16_t *hs = static_cast<uint16_t*>(h), *xs = static_cast<uint16_t*>(x);
   switch (H / 64) {
-#define X(E) \
-  case E: \
-    hipLaunchKernelGGL(add_rmsnorm_parts_kernel<E>, dim3(rows), dim3(64), 0, st, parts, n_parts, wp, hs, wn, xs, rows, \
-                       eps); \
+#define NPX(E, NP)                                                                                          \
+  case NP:                                                                                                  \
+    hipLaunchKernelGGL((add_rmsnorm_parts_kernel<E, NP>), dim3(rows), dim3(64), 0, st, parts, wp, hs, wn, xs, rows, \
+                       eps);                                                                                \
+    break;
+#define X(E)                                             \
+  case E:                                                \
+    switch (n_parts) { NPX(E, 1) NPX(E, 2) NPX(E, 3) NPX(E, 4) } \
     break;
     X(4) X(8) X(12) X(16) X(24) X(32)
 #undef X
+#undef NPX
     default: return GSS_ERR_UNSUPPORTED;
   }
   return gss_launch_status();

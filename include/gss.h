@@ -74,13 +74,14 @@ const char* gss_status_string(int status);
 int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes);
 
 /* Split-KV policy of both attention kernels: about target_wgs / (bs * Hkv) key splits per sequence and kv head, each
- * covering at least min_tiles 64-token tiles (defaults 512 and 4; min_tiles <= 256). Process-wide; set it before
+ * covering at least min_tiles 64-token tiles (defaults 768 and 4; min_tiles <= 256). Process-wide; set it before
  * sizing workspaces, and keep it fixed while a cache is decoded (it is part of the key partition). */
 int gss_attn_set_split_policy(int target_wgs, int min_tiles);
 
 /* Kernel choice of both attention entry points: batches with bs * Hkv >= bs_hkv (default 16) run the wide kernel
- * (one workgroup per key split for all query rows, double-buffered stages), smaller ones the row-group kernel (the
- * rows of a split spread over up to ceil(R / 48) workgroups, which fills the chip from few splits). Process-wide
+ * (one workgroup per key split for all query rows, tiles streamed through a ring of LDS slots), smaller ones the
+ * row-group kernel (the rows of a split spread over up to ceil(R / 48) workgroups, which fills the chip from few
+ * splits). Process-wide
  * and, like the split policy, part of how a batch's keys are combined: keep it fixed while a cache is decoded.
  * No counterpart in the reference (a launch-shape knob of these kernels). */
 int gss_attn_set_wide_min(int bs_hkv);
@@ -365,7 +366,8 @@ int gss_add_rmsnorm(const void* a, const void* w_post, void* h, const void* w_ne
                     float eps, gss_stream_t stream);
 
 /* gss_add_rmsnorm with a = bf16(parts[0] + ... + parts[n_parts - 1]) (fp32, added in part order; parts
- * [n_parts][rows][H], 16-byte aligned, as gss_gemm_parts writes them). H / 64 must be a multiple of 4. */
+ * [n_parts][rows][H], 16-byte aligned, as gss_gemm_parts writes them). H / 64 must be a multiple of 4;
+ * 1 <= n_parts <= 4 (gss_gemm_parts writes at most 2), else GSS_ERR_UNSUPPORTED. */
 int gss_add_rmsnorm_parts(const float* parts, int n_parts, const void* w_post, void* h, const void* w_next, void* x,
                           int rows, int H, float eps, gss_stream_t stream);
 
