@@ -70,6 +70,11 @@ def test_entry_points_reject_bad_arguments_before_launch():
     assert L.gss_gemm_set_policy(12, 16, 9) == ARG
     assert L.gss_attn_set_split_policy(0, 2) == ARG
     assert L.gss_attn_set_wide_min(0) == ARG
+    # the parts norm is built for 1..4 fp32 parts (gss_gemm_parts writes at most 2); dummy aligned pointers are
+    # never dereferenced on a rejected call
+    fake = ctypes.c_void_p(1 << 20)
+    assert L.gss_add_rmsnorm_parts(fake, 5, fake, fake, fake, fake, 17, 1536, 1e-5, null) == UNSUPPORTED
+    assert L.gss_add_rmsnorm_parts(fake, 0, fake, fake, fake, fake, 17, 1536, 1e-5, null) == ARG
 
 
 REFERENCE_SIGNATURES = {

@@ -91,6 +91,17 @@ def test_window_sizes(cuda, W):
     run_case(cuda, [777], W, 1, seed=W, verify=True)
 
 
+def test_many_ragged_sequences(cuda):
+    """More sequences than one wave scans at a time (the wide kernel finds its unit by a prefix scan over the batch in
+    chunks of 64 sequences), with empty, one-key and tile-boundary prefixes among them, on both kernels."""
+    rng = np.random.default_rng(70)
+    Ls = [int(x) for x in rng.integers(0, 600, size=70)]
+    Ls[0], Ls[5], Ls[63], Ls[64], Ls[69] = 0, 1, 64, 0, 1199
+    print(f"bs={len(Ls)}", flush=True)
+    run_case(cuda, Ls, 17, 1, max_kv_len=1300, seed=70)
+    run_case(cuda, Ls, 5, 1, max_kv_len=1300, seed=71, verify=True)
+
+
 def test_ragged_batch_and_capacity(cuda):
     # ragged prefixes, a capacity (max_kv_len) far above the actual lengths, as a captured graph would use
     run_case(cuda, [1024, 3, 4097, 0, 12288], 17, 1, max_kv_len=16384, seed=3)

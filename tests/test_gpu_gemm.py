@@ -261,6 +261,28 @@ def test_gemm_parts_parity_and_invariance(cuda, M, N, Kd):
         assert S == 2 and torch.equal(y, (parts[0] + parts[1]).bfloat16())
 
 
+@pytest.mark.parametrize("n_parts", [1, 2, 3, 4])
+def test_parts_norm_every_part_count(cuda, n_parts):
+    """gss_add_rmsnorm_parts for each part count it is built for == gss_add_rmsnorm on a = bf16 of the parts added in
+    part order (fp32), bit for bit."""
+    from gravityocr_amd.kernels import add_rmsnorm, add_rmsnorm_parts
+    g = torch.Generator().manual_seed(90 + n_parts)
+    M, H, eps = 17, 1536, 1e-5
+    parts = torch.randn(n_parts, M, H, generator=g).to(cuda)
+    h = torch.randn(M, H, generator=g).bfloat16().to(cuda)
+    wp = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16().to(cuda)
+    wn = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16().to(cuda)
+    a = parts[0].clone()
+    for k in range(1, n_parts):
+        a += parts[k]
+    h_ref, x_ref = h.clone(), torch.empty_like(h)
+    add_rmsnorm(a.bfloat16(), wp, h_ref, wn, x_ref, eps)
+    h1, x1 = h.clone(), torch.empty_like(h)
+    add_rmsnorm_parts(parts, wp, h1, wn, x1, eps)
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h_ref) and torch.equal(x1, x_ref)
+
+
 @pytest.mark.parametrize("M", [1, 5, 12, 17])
 def test_norms_on_parts_equal_unfused(cuda, M):
     """gss_add_rmsnorm_parts == gss_add_rmsnorm on a = bf16(sum of the parts), and the gate_up prologue with a_parts
