@@ -1063,12 +1063,14 @@ int attn_entry(const void* q, const void* k_pages, const void* v_pages, const in
   const int NT = (p.R + 15) / 16;
   int ng;
   if (wide) {
-    // rows: NT N-tiles of 16 in RG row groups of TPG tiles, dealt to RW row waves (the first TPG % RW take one
-    // more): 1 -> one wave of 1, 9 (17-row window) -> 3,2,2,2, 17 -> groups of 12 (3,3,3,3) and 5 (padding past NT)
-    p.RW = min(RW_MAX, NT);
-    p.TPG = min(NT, RW_MAX * NGW_MAX);
+    // rows: NT N-tiles of 16 in RG row groups of TPG tiles (as even as the group count allows; tiles past NT are
+    // padding), dealt to RW row waves (the first TPG % RW take one more): 1 -> one wave of 1, 9 (17-row window) ->
+    // 3,2,2,2, 17 (33-row window) -> two groups of 9 (3,2,2,2; the last tile padding) rather than 12 and 5, whose
+    // padding would triple the second group's work
+    p.RG = (NT + RW_MAX * NGW_MAX - 1) / (RW_MAX * NGW_MAX);
+    p.TPG = (NT + p.RG - 1) / p.RG;
+    p.RW = min(RW_MAX, p.TPG);
     ng = (p.TPG + p.RW - 1) / p.RW;
-    p.RG = (NT + p.TPG - 1) / p.TPG;
   } else {
     // row groups of ng <= RG_NTG N-tiles, one workgroup each
     ng = min(RG_NTG, NT);
