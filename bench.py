@@ -70,7 +70,8 @@ def attn_roofline(dev, L, W, cap, n_causal=1, copies=ATTN_COPIES, Hq=16, Hkv=2, 
 def attn_batched_roofline(dev, W=17, bs=32, copies=2, Hq=16, Hkv=2, D=128, seed=3):
     """The batched draft attention (bs sequences, prefixes L_i ~ U[1024, 12288] with a seeded generator, one shared
     pool of 16-token pages in shuffled order, window W): average call duration over ``copies`` distinct pools (each
-    ~0.4 GB, together more than the Infinity Cache). Returns (microseconds per call, algorithmic bytes per call)."""
+    ~0.4 GB, together more than the Infinity Cache). Returns (microseconds per call, algorithmic bytes per call,
+    flops of the two contractions per call)."""
     from gravityocr_amd import kernels as K
     Ls = np.random.default_rng(seed).integers(1024, 12289, size=bs)
     cap = int(Ls.max()) + W + 64
@@ -93,7 +94,8 @@ def attn_batched_roofline(dev, W=17, bs=32, copies=2, Hq=16, Hkv=2, D=128, seed=
                                                    max_kv_len=cap, workspace=ws) for kp, vp in pools]
     us = time_kernel(fns, n=4, reps=3)
     nbytes = sum(2 * Hkv * D * 2 * (int(L) + W) for L in Ls) + 2 * bs * W * Hq * D * 2
-    return us, nbytes
+    flops = sum(attn_flops(int(L), W, Hq, D) for L in Ls)
+    return us, nbytes, flops
 
 
 def copy_calibration(dev, reps=3):
@@ -179,7 +181,7 @@ def main():
                           "copy_bytes": COPY_BYTES}), flush=True)
         return
     if args.attn_batched_only:
-        b_us, b_bytes = attn_batched_roofline(torch.device("cuda:0"), W=args.bd + 1)
+        b_us, b_bytes, _ = attn_batched_roofline(torch.device("cuda:0"), W=args.bd + 1)
         print(json.dumps({"kernel": "gss_draft_attn batched", "W": args.bd + 1, "avg_us": round(b_us, 2),
                           "algorithmic_bytes": b_bytes, "achieved_GBs": round(b_bytes / (b_us * 1e-6) / 1e9, 1)}),
               flush=True)
@@ -366,8 +368,17 @@ def main():
     achieved = ab / (d_us * 1e-6) / 1e9
     tflops = attn_flops(L, Kw) / (d_us * 1e-6) / 1e12
     log(f"draft attention L={L}: {d_us:.2f} us, {achieved:.0f} GB/s, {tflops:.1f} TFLOP/s; verify {v_us:.2f} us")
-    b_us, b_bytes = attn_batched_roofline(dev)
-    log(f"batched draft attention (32 ragged sequences): {b_us:.2f} us, {b_bytes / (b_us * 1e-6) / 1e9:.0f} GB/s")
+    by_block = {}
+    for bdb in (8, 16, 32):  # the batched config's block sizes: windows of B + 1 rows
+        u, nb, fl = attn_batched_roofline(dev, W=bdb + 1)
+        by_block[str(bdb)] = {"avg_us": round(u, 2), "GBs": round(nb / (u * 1e-6) / 1e9, 1),
+                              "frac": round(nb / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                              "mfma_tflops": round(fl / (u * 1e-6) / 1e12, 1),
+                              "mfma_frac": round(fl / (u * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+        if bdb == 16:
+            b_us, b_bytes, b_flops = u, nb, fl
+    log(f"batched draft attention (32 ragged sequences): {b_us:.2f} us, {b_bytes / (b_us * 1e-6) / 1e9:.0f} GB/s; "
+        f"by block size {by_block}")
 
     # ---- CPU baseline: the oracle's round on the host cores, from the same 8K state -----------------------------
     cpu = None
@@ -432,7 +443,10 @@ def main():
                                                        "U[1024, 12288] (seed 3), W=17, one paged pool",
                              "achieved": round(b_bytes / (b_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(b_bytes / (b_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                             "algorithmic_bytes": b_bytes, "avg_us": round(b_us, 2)},
+                             "algorithmic_bytes": b_bytes, "avg_us": round(b_us, 2),
+                             "mfma_tflops": round(b_flops / (b_us * 1e-6) / 1e12, 1),
+                             "mfma_frac": round(b_flops / (b_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                             "by_block_size": by_block},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
