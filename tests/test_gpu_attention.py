@@ -84,11 +84,19 @@ def test_draft_mask_edges(cuda, L, n_causal):
     run_case(cuda, [L], 17, n_causal, seed=L + 7)
 
 
-@pytest.mark.parametrize("W", [1, 2, 5, 9, 33, 34])
+@pytest.mark.parametrize("W", [1, 2, 5, 9, 33, 34, 64])
 def test_window_sizes(cuda, W):
     print(f"W={W}", flush=True)
     run_case(cuda, [777], W, 1, seed=W)
     run_case(cuda, [777], W, 1, seed=W, verify=True)
+
+
+def test_no_grouping_and_wide_windows(cuda):
+    """Hq == Hkv (one query row per window row: the wide kernel runs a single row wave of two waves) and the widest
+    window (64 rows x 8 heads = 32 N-tiles: three row groups of 11)."""
+    run_case(cuda, [900, 31], 17, 1, Hq=2, Hkv=2, seed=80)
+    run_case(cuda, [900, 31], 64, 64, Hq=2, Hkv=2, seed=81, verify=True)
+    run_case(cuda, [2000, 70], 64, 1, seed=82)
 
 
 def test_many_ragged_sequences(cuda):
