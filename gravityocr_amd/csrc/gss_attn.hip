@@ -940,9 +940,9 @@ __global__ void __launch_bounds__(64) window_attn_merge(AttnParams p) {
 // on the same cache and batch size partitions the keys identically: about target_wgs / (bs * Hkv) splits per
 // sequence and kv head, each at least min_tiles tiles (gss_attn_set_split_policy). At bs = 1 the minimum decides
 // (short splits fill the chip); a large batch gets few long splits, which keeps the partial traffic and the merge
-// small (32 ragged sequences of up to 12K keys with a 17-row window: 12 splits of 17 tiles, 93 us per call, against
-// 122 us for 8 of 25 and 109 us for 15 of 13).
-int g_target_wgs = 768, g_min_tiles = 4;
+// small (32 ragged sequences of up to 12K keys with a 17-row window: 14 splits of 14 tiles, 87 us per call, against
+// 90 us for 12 of 17, 122 us for 8 of 25 and 107-113 us for 15 or 16 splits of 13).
+int g_target_wgs = 896, g_min_tiles = 4;
 int g_wide_min = 16;  // batches with bs * Hkv >= this run the wide kernel (gss_attn_set_wide_min)
 
 int attn_plan(int bs, int Hkv, int max_kv_len, int* n_split, int* tps) {

@@ -9,7 +9,7 @@ from ._lib import NormEpilogue, NormPrologue, Penalties, check, lib
 
 PAGE = 16
 # the attention kernels' library defaults (gss_attn_set_split_policy, gss_attn_set_wide_min)
-ATTN_POLICY = (768, 4)
+ATTN_POLICY = (896, 4)
 ATTN_WIDE_MIN = 16
 
 

@@ -74,7 +74,7 @@ const char* gss_status_string(int status);
 int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes);
 
 /* Split-KV policy of both attention kernels: about target_wgs / (bs * Hkv) key splits per sequence and kv head, each
- * covering at least min_tiles 64-token tiles (defaults 768 and 4; min_tiles <= 256). Process-wide; set it before
+ * covering at least min_tiles 64-token tiles (defaults 896 and 4; min_tiles <= 256). Process-wide; set it before
  * sizing workspaces, and keep it fixed while a cache is decoded (it is part of the key partition). */
 int gss_attn_set_split_policy(int target_wgs, int min_tiles);
 
