@@ -15,11 +15,10 @@ _psz = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES = {
     "gss_version": ([], ctypes.c_char_p),
     "gss_status_string": ([_i], ctypes.c_char_p),
-    "gss_attn_workspace_size": ([_i, _i, _i, _i, _i, _i, _psz], _i),
-    "gss_attn_set_split_policy": ([_i, _i], _i),
-    "gss_attn_set_wide_min": ([_i], _i),
-    "gss_draft_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
-    "gss_verify_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _i, _p, _sz, _p], _i),
+    "gss_attn_make_plan": ([_i, _i, _i, _i, _i, _i, _p], _i),
+    "gss_attn_workspace_size": ([_i, _i, _i, _i, _i, _p, _psz], _i),
+    "gss_draft_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _i, _f, _p, _p, _sz, _p], _i),
+    "gss_verify_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _p, _sz, _p], _i),
     "gss_argmax_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_argmax_accept": ([_p, _i, _i64, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
     "gss_unmask_workspace_size": ([_i, _i, _i, _psz], _i),
@@ -32,7 +31,6 @@ SIGNATURES = {
     "gss_penalize_rows": ([_p, _i64, _i, _i, _i, _p, _p, _p], _i),
     "gss_sample_workspace_size": ([_i, _i, _psz], _i),
     "gss_sample_rows": ([_p, _i64, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
-    "gss_gemm_set_policy": ([_i, _i, _i], _i),
     "gss_gemm_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_gemm": ([_p, _i64, _p, _p, _i64, _p, _i64, _i, _i, _i, _i, _p, _p, _sz, _p], _i),
     "gss_gemm_parts_count": ([_i, _i, ctypes.POINTER(ctypes.c_int)], _i),
@@ -49,6 +47,18 @@ SIGNATURES = {
     "gss_silu_mul": ([_p, _i64, _p, _i, _i, _p], _i),
 }
 
+
+
+class AttnPlan(ctypes.Structure):
+    """gss_attn_plan (include/gss.h): the attention kernel and key partition of a batch shape."""
+    _fields_ = [("kernel", ctypes.c_int), ("tiles_per_split", ctypes.c_int), ("n_split", ctypes.c_int),
+                ("max_kv_len", ctypes.c_int)]
+
+    def key(self):
+        return (self.kernel, self.tiles_per_split, self.n_split, self.max_kv_len)
+
+    def __repr__(self):
+        return "AttnPlan(kernel=%d, tiles_per_split=%d, n_split=%d, max_kv_len=%d)" % self.key()
 
 
 class NormEpilogue(ctypes.Structure):

@@ -26,9 +26,9 @@
 //   * Grid order is XCD-aware: the grid enumerates only the units that hold keys (each workgroup finds its unit from
 //     the device-side lengths), consecutive units go to different XCDs (ragged batches balance), the row groups of
 //     one unit to the same XCD (their repeated K/V reads hit its L2).
-//   * Keys are tiled by absolute position (window rows take the positions after the prefix); the split size and
-//     the tile -> split -> key lane assignment depend only on the capacity max_kv_len and on fixed constants, never
-//     on W, the prefix length or the row grouping, and every combine runs in a fixed order. Results therefore do not
+//   * Keys are tiled by absolute position (window rows take the positions after the prefix); the split size, the
+//     tile -> split -> key lane assignment and the kernel come from the caller's plan (gss_attn_plan) only, never
+//     from W, the prefix length or the row grouping, and every combine runs in a fixed order. Results therefore do not
 //     depend on where a key comes from or on how many rows are in the window: a verify row reproduces the AR step
 //     of the same token bit for bit. With several splits, the normalized partial O (bf16) and (m, l) (fp32) of each
 //     split go to the caller's workspace and the merge kernel combines the valid splits of every row.
@@ -70,6 +70,7 @@ struct AttnParams {
   uint16_t* ws_o;  // [bs, Hkv, n_split, R, D] bf16: O / l of each split
   float* ws_ml;    // [bs, Hkv, R, n_split, 2]:      (m, l) of each split (log2 domain max, sum)
   int bs, pt_stride, prefix_extra, W, n_causal, Hq, Hkv, G, R, n_split, RW, TPG, RG, n_units, tps;
+  int cap;  // prefix lengths are clamped to this: min(plan capacity, what a page-table row addresses)
   float scale_log2;
 };
 
@@ -234,7 +235,7 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
       const int bb = c + lane;
       int nvb = 0;  // valid splits of sequence bb
       if (bb < p.bs) {
-        const int Lb = min(max(p.prefix_len[bb] + p.prefix_extra, 0), p.pt_stride * PAGE);
+        const int Lb = min(max(p.prefix_len[bb] + p.prefix_extra, 0), p.cap);
         nvb = min(p.n_split, valid_splits(Lb, p.W, p.tps));
       }
       int inc = nvb * p.Hkv;  // inclusive prefix sum of the chunk's unit counts
@@ -268,8 +269,9 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   if (b < 0) return;  // past the last valid unit
   const int kl = wv % KL, rw = wv / KL;                       // key lane, row wave
   const int l16 = lane & 15, g4 = lane >> 4;
-  // committed prefix length; clamped to what the page-table row can address so every page-table read is in bounds
-  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.pt_stride * PAGE);
+  // committed prefix length; clamped to the plan's capacity and to what the page-table row can address, so every
+  // key falls in one of the plan's splits and every page-table read is in bounds
+  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.cap);
   const int W = p.W, nc = p.n_causal;
   const int n_tiles = (L + W + TILE - 1) / TILE;
   const int t_beg = s * p.tps, t_end = min(n_tiles, t_beg + p.tps);
@@ -602,8 +604,9 @@ __global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kq = wv >> 1, half = wv & 1;                      // tile lane, key half (32 keys) of this wave
   const int l16 = lane & 15, g4 = lane >> 4;
-  // committed prefix length; clamped to what the page-table row can address so every page-table read is in bounds
-  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.pt_stride * PAGE);
+  // committed prefix length; clamped to the plan's capacity and to what the page-table row can address, so every
+  // key falls in one of the plan's splits and every page-table read is in bounds
+  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.cap);
   const int W = p.W, nc = p.n_causal;
   const int n_tiles = (L + W + TILE - 1) / TILE;
   const int t_beg = s * p.tps, t_end = min(n_tiles, t_beg + p.tps);
@@ -868,7 +871,7 @@ __global__ void __launch_bounds__(64) window_attn_merge(AttnParams p) {
   const int64_t ostride = static_cast<int64_t>(p.R) * D;
   // one round of loads: the length, and (m, l) and the first PRE * SGW partial rows of every split of the workspace
   // (in bounds whatever the length); the valid count masks them afterwards
-  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.pt_stride * PAGE);
+  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.cap);
   float2 mlv[MLR];
 #pragma unroll
   for (int k = 0; k < MLR; ++k) {
@@ -936,27 +939,47 @@ __global__ void __launch_bounds__(64) window_attn_merge(AttnParams p) {
                                              cvt_pk_bf16(acc[4] * inv, acc[5] * inv), cvt_pk_bf16(acc[6] * inv, acc[7] * inv)};
 }
 
-// Split sizing: tiles per split from the capacity (max_kv_len plus a full window) and bs * Hkv only, so every call
-// on the same cache and batch size partitions the keys identically: about target_wgs / (bs * Hkv) splits per
-// sequence and kv head, each at least min_tiles tiles (gss_attn_set_split_policy). At bs = 1 the minimum decides
-// (short splits fill the chip); a large batch gets few long splits, which keeps the partial traffic and the merge
-// small (32 ragged sequences of up to 12K keys with a 17-row window: 14 splits of 14 tiles, 87 us per call, against
-// 90 us for 12 of 17, 122 us for 8 of 25 and 107-113 us for 15 or 16 splits of 13).
-int g_target_wgs = 896, g_min_tiles = 4;
-int g_wide_min = 16;  // batches with bs * Hkv >= this run the wide kernel (gss_attn_set_wide_min)
+// Default plan (gss_attn_make_plan with zeros): about DEF_TARGET_WGS / (bs * Hkv) key splits per sequence and kv
+// head, each at least DEF_MIN_TILES tiles; batches with bs * Hkv >= DEF_WIDE_MIN run the wide kernel. At bs = 1 the
+// minimum decides (short splits fill the chip); a large batch gets few long splits, which keeps the partial traffic
+// and the merge small (32 ragged sequences of up to 12K keys with a 17-row window: 14 splits of 14 tiles, 87 us per
+// call, against 90 us for 12 of 17, 122 us for 8 of 25 and 107-113 us for 15 or 16 splits of 13).
+constexpr int DEF_TARGET_WGS = 896, DEF_MIN_TILES = 4, DEF_WIDE_MIN = 16;
 
-int attn_plan(int bs, int Hkv, int max_kv_len, int* n_split, int* tps) {
-  const int tiles = (max(max_kv_len, 0) + TILE + TILE - 1) / TILE;
-  const int by_chip = max(1, (g_target_wgs + bs * Hkv - 1) / (bs * Hkv));
-  int t = max(g_min_tiles, (tiles + by_chip - 1) / by_chip);
+// The plan fixes the key partition (tiles by absolute position, tiles_per_split of them per split) and the kernel;
+// both depend on the arguments here only, never on W or on the lengths of a call.
+int make_plan(int bs, int Hkv, int max_kv_len, int target_wgs, int min_tiles, int wide_min, gss_attn_plan* plan) {
+  if (!plan || bs <= 0 || Hkv <= 0 || max_kv_len < 0 || target_wgs < 0 || min_tiles < 0 || wide_min < 0)
+    return GSS_ERR_ARG;
+  if (min_tiles > MAX_TPS) return GSS_ERR_ARG;
+  if (target_wgs == 0) target_wgs = DEF_TARGET_WGS;
+  if (min_tiles == 0) min_tiles = DEF_MIN_TILES;
+  if (wide_min == 0) wide_min = DEF_WIDE_MIN;
+  const int tiles = (max_kv_len + TILE + TILE - 1) / TILE;  // the capacity plus a full window
+  const int by_chip = max(1, (target_wgs + bs * Hkv - 1) / (bs * Hkv));
+  int t = max(min_tiles, (tiles + by_chip - 1) / by_chip);
   int ns = (tiles + t - 1) / t;
   if (ns > MAX_SPLIT) {
     ns = MAX_SPLIT;
     t = (tiles + ns - 1) / ns;
   }
   if (t > MAX_TPS) return GSS_ERR_UNSUPPORTED;
-  *n_split = (tiles + t - 1) / t;
-  *tps = t;
+  plan->kernel = bs * Hkv >= wide_min ? GSS_ATTN_WIDE : GSS_ATTN_ROWGROUP;
+  plan->tiles_per_split = t;
+  plan->n_split = (tiles + t - 1) / t;
+  plan->max_kv_len = max_kv_len;
+  return GSS_OK;
+}
+
+// A caller-filled plan is accepted when its splits cover the capacity plus a full window.
+int check_plan(const gss_attn_plan* plan) {
+  if (!plan) return GSS_ERR_ARG;
+  if (plan->kernel != GSS_ATTN_ROWGROUP && plan->kernel != GSS_ATTN_WIDE) return GSS_ERR_ARG;
+  if (plan->tiles_per_split < 1 || plan->tiles_per_split > MAX_TPS || plan->n_split < 1 ||
+      plan->n_split > MAX_SPLIT || plan->max_kv_len < 0)
+    return GSS_ERR_ARG;
+  const int64_t tiles = (static_cast<int64_t>(plan->max_kv_len) + TILE + TILE - 1) / TILE;
+  if (static_cast<int64_t>(plan->n_split) * plan->tiles_per_split < tiles) return GSS_ERR_ARG;
   return GSS_OK;
 }
 
@@ -1031,12 +1054,13 @@ size_t ws_bytes(int bs, int Hkv, int R, int D, int n_split) {
 
 int attn_entry(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int pt_stride,
                const int32_t* prefix_len, int prefix_extra, const void* k_win, const void* v_win, void* out, int bs,
-               int W, int n_causal, int Hq, int Hkv, int D, int page, float scale, int max_kv_len, void* workspace,
-               size_t workspace_bytes, hipStream_t st) {
+               int W, int n_causal, int Hq, int Hkv, int D, int page, float scale, const gss_attn_plan* plan,
+               void* workspace, size_t workspace_bytes, hipStream_t st) {
   int rc = validate(bs, W, Hq, Hkv, D, page);
   if (rc != GSS_OK) return rc;
+  if ((rc = check_plan(plan)) != GSS_OK) return rc;
   if (!q || !k_pages || !v_pages || !page_table || !prefix_len || !k_win || !v_win || !out) return GSS_ERR_ARG;
-  if (n_causal < 0 || max_kv_len < 0 || pt_stride <= 0) return GSS_ERR_ARG;
+  if (n_causal < 0 || pt_stride <= 0) return GSS_ERR_ARG;
   AttnParams p;
   p.q = static_cast<const uint16_t*>(q);
   p.k_pages = static_cast<const uint16_t*>(k_pages);
@@ -1054,12 +1078,13 @@ int attn_entry(const void* q, const void* k_pages, const void* v_pages, const in
   p.Hkv = Hkv;
   p.G = Hq / Hkv;
   p.R = p.G * W;
-  rc = attn_plan(bs, Hkv, max_kv_len, &p.n_split, &p.tps);
-  if (rc != GSS_OK) return rc;
+  p.n_split = plan->n_split;
+  p.tps = plan->tiles_per_split;
+  p.cap = static_cast<int>(min(static_cast<int64_t>(plan->max_kv_len), static_cast<int64_t>(pt_stride) * PAGE));
   p.bs = bs;
   p.n_units = bs * Hkv * p.n_split;
-  // kernel: a function of the batch shape only (never of W), so every window size of one batch runs the same one
-  const bool wide = bs * Hkv >= g_wide_min;
+  // kernel: the plan's (never a function of W), so every window size of one batch runs the same one
+  const bool wide = plan->kernel == GSS_ATTN_WIDE;
   const int NT = (p.R + 15) / 16;
   int ng;
   if (wide) {
@@ -1092,47 +1117,36 @@ int attn_entry(const void* q, const void* k_pages, const void* v_pages, const in
 
 }  // namespace
 
-extern "C" int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes) {
+extern "C" int gss_attn_make_plan(int bs, int Hkv, int max_kv_len, int target_wgs, int min_tiles, int wide_min,
+                                  gss_attn_plan* plan) {
+  return make_plan(bs, Hkv, max_kv_len, target_wgs, min_tiles, wide_min, plan);
+}
+
+extern "C" int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, const gss_attn_plan* plan,
+                                       size_t* bytes) {
   if (!bytes) return GSS_ERR_ARG;
   int rc = validate(bs, W, Hq, Hkv, D, PAGE);
   if (rc != GSS_OK) return rc;
-  if (max_kv_len < 0) return GSS_ERR_ARG;
-  int ns, tps;
-  rc = attn_plan(bs, Hkv, max_kv_len, &ns, &tps);
-  if (rc != GSS_OK) return rc;
-  *bytes = ws_bytes(bs, Hkv, (Hq / Hkv) * W, D, ns);
+  if ((rc = check_plan(plan)) != GSS_OK) return rc;
+  *bytes = ws_bytes(bs, Hkv, (Hq / Hkv) * W, D, plan->n_split);
   return GSS_OK;
 }
 
 extern "C" int gss_draft_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
                               int pt_stride, const int32_t* prefix_len, int prefix_extra, const void* k_win,
                               const void* v_win, void* out, int bs, int W, int n_causal, int Hq, int Hkv, int D,
-                              int page, float scale, int max_kv_len, void* workspace, size_t workspace_bytes,
-                              gss_stream_t stream) {
+                              int page, float scale, const gss_attn_plan* plan, void* workspace,
+                              size_t workspace_bytes, gss_stream_t stream) {
   return attn_entry(q, k_pages, v_pages, page_table, pt_stride, prefix_len, prefix_extra, k_win, v_win, out, bs, W,
-                    n_causal, Hq, Hkv, D, page, scale, max_kv_len, workspace, workspace_bytes,
+                    n_causal, Hq, Hkv, D, page, scale, plan, workspace, workspace_bytes,
                     static_cast<hipStream_t>(stream));
 }
 
 extern "C" int gss_verify_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
                                int pt_stride, const int32_t* prefix_len, int prefix_extra, const void* k_win,
                                const void* v_win, void* out, int bs, int W, int Hq, int Hkv, int D, int page,
-                               float scale, int max_kv_len, void* workspace, size_t workspace_bytes,
+                               float scale, const gss_attn_plan* plan, void* workspace, size_t workspace_bytes,
                                gss_stream_t stream) {
   return attn_entry(q, k_pages, v_pages, page_table, pt_stride, prefix_len, prefix_extra, k_win, v_win, out, bs, W,
-                    W, Hq, Hkv, D, page, scale, max_kv_len, workspace, workspace_bytes,
-                    static_cast<hipStream_t>(stream));
-}
-
-extern "C" int gss_attn_set_wide_min(int bs_hkv) {
-  if (bs_hkv < 1) return GSS_ERR_ARG;
-  g_wide_min = bs_hkv;
-  return GSS_OK;
-}
-
-extern "C" int gss_attn_set_split_policy(int target_wgs, int min_tiles) {
-  if (target_wgs < 1 || min_tiles < 1 || min_tiles > MAX_TPS) return GSS_ERR_ARG;
-  g_target_wgs = target_wgs;
-  g_min_tiles = min_tiles;
-  return GSS_OK;
+                    W, Hq, Hkv, D, page, scale, plan, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
 }

@@ -1,6 +1,8 @@
-// Skinny GEMM for the decode forwards: Y[M, N] = X[M, Kd] . W[N, Kd]^T with M <= 64 rows (bs * window),
-// bf16 operands, fp32 accumulation. Weight streaming is the whole cost (N*Kd*2 bytes per call), so the kernel is
-// built to keep many 16-byte weight loads in flight and to touch every weight byte exactly once.
+// Skinny GEMM for the decode forwards: Y[M, N] = X[M, Kd] . W[N, Kd]^T with M = bs * window rows, bf16 operands,
+// fp32 accumulation. Weight streaming is the whole cost at M <= 64 (N*Kd*2 bytes per call), so the kernel is built
+// to keep many 16-byte weight loads in flight and to touch every weight byte exactly once. Batched windows (M > 64)
+// run as slabs of 64 rows: one workgroup per (column tile, slab), the slabs of a tile back to back on one XCD so
+// they share its weights through that XCD's L2.
 //
 // Layout on v_mfma_f32_16x16x32_bf16: A = 16 weight rows x 32 k (lane: row l%16, k 8*(l/16)..+7, one 16-byte
 // load), B = 32 k x 16 activation rows (lane: activation row l%16, same k), C = Y^T tile (lane: 4 consecutive
@@ -8,8 +10,9 @@
 // contiguous ranges and reduce their partial tiles through LDS in wave order.
 //
 // Batch invariance: an output element is always the same sequence of MFMA k-steps and the same wave-order
-// reduction, whatever M is and wherever its row sits, so a row computed in a 17-row verify forward is bit-identical
-// to the same row computed alone (a 1-row AR step). Decode parity between speculative and AR decoding rests on it.
+// reduction, whatever M is and wherever its row sits (in which slab, at which row of it), so a row computed in a
+// 17-row verify forward or a 544-row batched verify is bit-identical to the same row computed alone (a 1-row AR
+// step). Decode parity between speculative and AR decoding rests on it.
 //
 // Fused epilogues (the GEMM output is rounded to bf16 first, as a bf16 torch linear writes it):
 //   EPI_PLAIN   Y bf16 (or fp32) [M, ldy]
@@ -63,7 +66,26 @@ struct GemmParams {
   uint16_t* post_x;
   float post_eps;
   uint32_t* done_ctr;
+  // row slabs: M > 64 rows run as n_slabs slabs of up to 64 rows, one workgroup per (column tile, slab), each
+  // computing exactly what a call with the slab's rows alone computes (tile_slab gives the mapping)
+  int n_slabs;
+  int slab_xcd;  // 1: the slabs of one column tile run back to back on one XCD (needs n_tiles % 8 == 0)
 };
+
+// Column tile and row slab of workgroup x of gemm_kernel. Workgroups are dealt to the 8 XCDs round-robin by linear
+// index; with slab_xcd the n_slabs slabs of a column tile get consecutive indices on one XCD (x % 8 == tile % 8), so
+// the later slabs read the tile's weights from that XCD's L2 instead of HBM.
+struct TileSlab {
+  int tile, slab;
+};
+GSS_DEV TileSlab tile_slab(const GemmParams& p, int x) {
+  if (p.n_slabs == 1) return {x, 0};
+  if (p.slab_xcd) {
+    const int j = x / 8;
+    return {(j / p.n_slabs) * 8 + x % 8, j % p.n_slabs};
+  }
+  return {x / p.n_slabs, x % p.n_slabs};
+}
 
 constexpr int MAX_NW = 12;  // waves per workgroup (768 threads: 168 VGPRs per lane)
 constexpr size_t MAX_LDS = 160 * 1024;  // LDS per workgroup on gfx950
@@ -228,12 +250,12 @@ GSS_DEV void post_addnorm_row(const GemmParams& p, int row, int lane) {
   }
 }
 
-// Epilogue of output tile (f, n) of the workgroup whose first feature is f0, on its reduced sum s (lane: activation
-// row n*16 + l16, features f0 + f*16 + g4*4 .. +3). The GEMM output is rounded to bf16 first, as a bf16 torch linear
-// writes it.
+// Epilogue of output tile (f, n) of the workgroup whose first feature is f0 and first row row0, on its reduced sum s
+// (lane: activation row row0 + n*16 + l16, features f0 + f*16 + g4*4 .. +3). The GEMM output is rounded to bf16
+// first, as a bf16 torch linear writes it.
 template <int EPI, bool POST>
-GSS_DEV void gemm_epilogue(const GemmParams& p, int f0, int f, int n, floatx4_t s, int l16, int g4) {
-  const int row = n * 16 + l16;            // activation row
+GSS_DEV void gemm_epilogue(const GemmParams& p, int f0, int row0, int f, int n, floatx4_t s, int l16, int g4) {
+  const int row = row0 + n * 16 + l16;     // activation row
   const int feat = f0 + f * 16 + g4 * 4;   // first of this lane's 4 consecutive output features
   float y0 = s[0], y1 = s[1], y2 = s[2], y3 = s[3];
   if constexpr (EPI == EPI_PLAIN) {
@@ -289,7 +311,11 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   extern __shared__ floatx4_t red[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
-  const int f0 = blockIdx.x * FT * 16;
+  const TileSlab ts = tile_slab(p, blockIdx.x);
+  const int f0 = ts.tile * FT * 16;
+  // this workgroup's rows: [row0, row0 + Ms); everything below sees only them (x, the staging, the epilogue)
+  const int row0 = ts.slab * 64, Ms = min(64, p.M - row0);
+  const uint16_t* xs0 = p.x + static_cast<int64_t>(row0) * p.ldx;
   const int ksteps = p.Kd / 32;
   const int ks = blockIdx.y;  // k split: k-steps [ks * kps, (ks + 1) * kps)
   const int k_end = min(ksteps, (ks + 1) * p.kps);
@@ -312,17 +338,17 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
 #pragma unroll
   for (int n = 0; n < NT; ++n) {
     const int r = n * 16 + l16;
-    xlive[n] = r < p.M;
-    xrow[n] = p.x + static_cast<int64_t>(xlive[n] ? r : 0) * p.ldx + g4 * 8;
+    xlive[n] = r < Ms;
+    xrow[n] = xs0 + static_cast<int64_t>(xlive[n] ? r : 0) * p.ldx + g4 * 8;
   }
 
   uint16_t* xs = reinterpret_cast<uint16_t*>(red + NW * FT * NT * 64);
   const int cpr = ksw * 4;
-  uint16_t* xw = xs + wv * p.M * cpr * 8;  // XS: this wave's staged rows
+  uint16_t* xw = xs + wv * Ms * cpr * 8;  // XS: this wave's staged rows
   if constexpr (XS) {
-    // one pass (ksw <= UNR): rows 0..M-1, k-steps [s_beg, s_end) -> LDS, issued before the weight loads below
-    const int n_slots = p.M * cpr, live_chunks = (s_end - s_beg) * 4;
-    const uint16_t* xbase = p.x + static_cast<int64_t>(s_beg) * 32;
+    // one pass (ksw <= UNR): rows 0..Ms-1, k-steps [s_beg, s_end) -> LDS, issued before the weight loads below
+    const int n_slots = Ms * cpr, live_chunks = (s_end - s_beg) * 4;
+    const uint16_t* xbase = xs0 + static_cast<int64_t>(s_beg) * 32;
 #pragma unroll 1
     for (int j = 0; j * 64 < n_slots; ++j) {
       const int q = j * 64 + lane;
@@ -403,13 +429,13 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   __syncthreads();
 
   // epilogue of tile (f, n) on its reduced sum (wave v owns the tiles with (f * NT + n) % NW == v)
-  auto epilogue = [&](int f, int n, floatx4_t s) { gemm_epilogue<EPI, POST>(p, f0, f, n, s, l16, g4); };
+  auto epilogue = [&](int f, int n, floatx4_t s) { gemm_epilogue<EPI, POST>(p, f0, row0, f, n, s, l16, g4); };
   auto reduced = [&](int f, int n) {
     floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
     for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
     return s;
   };
-  auto live = [&](int f, int n) { return n * 16 + l16 < p.M && f0 + f * 16 + g4 * 4 < p.N; };
+  auto live = [&](int f, int n) { return n * 16 + l16 < Ms && f0 + f * 16 + g4 * 4 < p.N; };
   __shared__ int last_flag;
 
   if constexpr (EPI == EPI_PARTS) {
@@ -420,7 +446,7 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
       for (int n = 0; n < NT; ++n)
         if ((f * NT + n) % NW == wv && live(f, n))
           *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) +
-                                        (static_cast<int64_t>(ks) * p.M + n * 16 + l16) * p.ldy + f0 + f * 16 +
+                                        (static_cast<int64_t>(ks) * p.M + row0 + n * 16 + l16) * p.ldy + f0 + f * 16 +
                                         g4 * 4) = reduced(f, n);
     return;
   }
@@ -435,7 +461,7 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
     // order and runs the epilogue, then resets the counter. Partials are agent-scope stores (written through to the
     // coherence point), waited for before the barrier and the counter bump; the last reads them with agent loads.
     auto part_at = [&](int k, int f, int n) {
-      return reinterpret_cast<uint64_t*>(p.part + (static_cast<int64_t>(k) * p.M + n * 16 + l16) * p.N + f0 +
+      return reinterpret_cast<uint64_t*>(p.part + (static_cast<int64_t>(k) * p.M + row0 + n * 16 + l16) * p.N + f0 +
                                          f * 16 + g4 * 4);
     };
 #pragma unroll
@@ -548,7 +574,7 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
         if ((f * NT + n) % NW != wv || n * 16 + l16 >= p.M || f0 + f * 16 + g4 * 4 >= p.N) continue;
         floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
         for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
-        gemm_epilogue<EPI, false>(p, f0, f, n, s, l16, g4);
+        gemm_epilogue<EPI, false>(p, f0, 0, f, n, s, l16, g4);
       }
   };
   // two register sets, alternating: while one tile is computed, the next one's weights stream into the other set.
@@ -597,10 +623,11 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
   }
 }
 
-// Launch shape knobs (process-wide): the most waves per workgroup, the features per workgroup (0 = automatic) and
-// the most k splits over workgroups (1 = none).
-int g_max_nw = MAX_NW, g_ft = 0, g_max_ksplit = 2;
-int g_stream_wgs = 0;  // workgroups of the persistent GEMM (0: the device's CU count)
+// Launch shape: the most k splits over workgroups of a plain GEMM (1 = none). Like every other launch-shape choice
+// it is a function of the weight shape (and the device's CU count) only: it fixes the reduction order, so it is a
+// constant, never a setting that could differ between two calls on the same weights.
+constexpr int MAX_KSPLIT = 2;
+constexpr int MAX_ROWS = 65536;  // rows of one call (slabs of 64)
 constexpr bool kStageX = true;  // stage the activations through LDS where it applies (gemm_kernel)
 
 // Dynamic LDS beyond the default 64 KB for kernel K (once per process, before its first launch).
@@ -613,7 +640,6 @@ bool allow_full_lds() {
 
 // workgroups of the persistent kernel: one per CU of the current device (queried once)
 int stream_wgs() {
-  if (g_stream_wgs > 0) return g_stream_wgs;
   static int cus = 0;
   if (cus == 0) {
     int dev = 0, n = 0;
@@ -635,11 +661,12 @@ constexpr size_t CTR_BYTES = (CTR_TILES + 64) * sizeof(uint32_t);
 // counter) costs more than the extra streaming width buys. A function of the weight shape only, so every M runs the
 // same reduction order. For the 1536-hidden decoder: down (Kd 4608) splits in 2, the other projections do not.
 int gemm_ksplit(int n_tiles, int ksteps) {
-  int ks = max(1, min(g_max_ksplit, 384 / max(1, n_tiles)));
+  int ks = max(1, min(MAX_KSPLIT, 384 / max(1, n_tiles)));
   return max(1, min(ks, ksteps / 64));
 }
 
-int gemm_ft(int N) { return (g_ft == 1 || (g_ft == 0 && N / 16 <= 2048)) ? 1 : 2; }
+// features per workgroup / 16: 1 unless that makes more than ~8 workgroups per CU (the LM head)
+int gemm_ft(int N) { return N / 16 <= 2048 ? 1 : 2; }
 
 // k splits of the partial-sum output (EPI_PARTS): up to 2, as many as keep the column tiles x splits within one
 // workgroup per CU, each split at least 4 k-steps. A function of the weight shape only (the reduction order).
@@ -660,19 +687,25 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
   const int n_tiles = (p.N + FT * 16 - 1) / (FT * 16);
   p.ksplit = EPI == EPI_PARTS ? gemm_parts_split(n_tiles, ksteps) : gemm_ksplit(n_tiles, ksteps);
   p.kps = (ksteps + p.ksplit - 1) / p.ksplit;
+  // rows beyond 64: slabs of 64 rows, each its own workgroup per column tile (the fused prologue and post-norm need
+  // every row in one workgroup, so they stay at M <= 64)
+  p.n_slabs = (p.M + 63) / 64;
+  p.slab_xcd = p.n_slabs > 1 && n_tiles % 8 == 0;
+  const int Mw = min(p.M, 64);  // rows of one workgroup
+  if ((PRO == PRO_ADDNORM || POST) && p.n_slabs > 1) return GSS_ERR_UNSUPPORTED;
   if ((p.ksplit > 1 && EPI != EPI_PARTS) || POST) {
-    if (n_tiles > CTR_TILES) return GSS_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(n_tiles) * p.n_slabs > CTR_TILES) return GSS_ERR_UNSUPPORTED;
     const size_t need = CTR_BYTES + (p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * p.M * p.N * sizeof(float) : 0);
     if (!ws || ws_bytes < need) return GSS_ERR_WORKSPACE;
     p.tile_ctr = static_cast<uint32_t*>(ws);
     p.done_ctr = p.tile_ctr + CTR_TILES;
     p.part = reinterpret_cast<float*>(static_cast<char*>(ws) + CTR_BYTES);
   }
-  // k-steps per wave: the fewest that cover a split with at most g_max_nw waves (rounded to a multiple of 4)
-  int ksw = (p.kps + g_max_nw - 1) / g_max_nw;
+  // k-steps per wave: the fewest that cover a split with at most MAX_NW waves (rounded to a multiple of 4)
+  int ksw = (p.kps + MAX_NW - 1) / MAX_NW;
   ksw = (ksw + 3) / 4 * 4;
   const int nw = (p.kps + ksw - 1) / ksw;
-  const dim3 grid(n_tiles, p.ksplit), block(64 * nw);
+  const dim3 grid(n_tiles * p.n_slabs, p.ksplit), block(64 * nw);
   size_t lds = static_cast<size_t>(nw) * FT * NT * 64 * sizeof(floatx4_t);
   if constexpr (PRO == PRO_ADDNORM) {
     lds += static_cast<size_t>(p.M) * (p.Kd + XPAD) * sizeof(uint16_t);
@@ -702,13 +735,13 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
       // more column tiles than CUs and one load pass per tile (a function of N and Kd only, so every row count
       // takes the same kernel): the persistent kernel, one workgroup per CU walking the tiles
       const int G = stream_wgs();
-      if (EPI != EPI_PARTS && p.ksplit == 1 && ksw <= 4 && n_tiles > G) {
+      if (EPI != EPI_PARTS && p.ksplit == 1 && ksw <= 4 && n_tiles > G && p.n_slabs == 1) {
         hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI>), dim3(G), block, lds, st, p, ksw, n_tiles);
         return gss_launch_status();
       }
     }
     // activations staged in LDS when a wave's k-range is one pass and the rows fit (same arithmetic either way)
-    const size_t lds_xs = lds + static_cast<size_t>(nw) * p.M * ksw * 64;
+    const size_t lds_xs = lds + static_cast<size_t>(nw) * Mw * ksw * 64;
     const bool xs = kStageX && lds_xs <= MAX_DYN_LDS;
     if constexpr (FT + NT <= 3) {
       if (ksw % 8 == 0) {
@@ -735,7 +768,7 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
 
 template <int EPI, int PRO, bool POST>
 int launch_epi(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
-  const int NT = (p.M + 15) / 16;
+  const int NT = (min(p.M, 64) + 15) / 16;  // row tiles of one workgroup (one 64-row slab)
   // 16 features per workgroup unless that makes more than ~8 workgroups per CU (the LM head)
   if (gemm_ft(p.N) == 1) {
     switch (NT) {
@@ -760,7 +793,7 @@ int launch_epi(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
 int gemm_entry(GemmParams& p, int epi, void* ws, size_t ws_bytes, hipStream_t st) {
   const bool pro = p.h_in != nullptr, post = p.post_h != nullptr;
   if ((!pro && !p.x) || !p.w || p.M <= 0 || p.N <= 0 || p.Kd <= 0) return GSS_ERR_ARG;
-  if (p.M > 64 || p.Kd % 32 != 0 || p.N % 16 != 0) return GSS_ERR_UNSUPPORTED;
+  if (p.M > MAX_ROWS || p.Kd % 32 != 0 || p.N % 16 != 0) return GSS_ERR_UNSUPPORTED;
   if (p.ldw < p.Kd || (p.ldw % 8) || (!pro && (p.ldx < p.Kd || (p.ldx % 8)))) return GSS_ERR_ARG;
   if ((reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.w)) & 15u) return GSS_ERR_ARG;
   if (post) {
@@ -916,14 +949,4 @@ extern "C" int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_pr
   p.v_out = static_cast<uint16_t*>(v_win);
   set_prologue(p, pro);
   return gemm_entry(p, EPI_ROPE, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
-}
-
-extern "C" int gss_gemm_set_policy(int max_waves, int features_per_wg, int max_ksplit) {
-  if (max_waves < 1 || max_waves > MAX_NW || (features_per_wg != 0 && features_per_wg != 16 && features_per_wg != 32))
-    return GSS_ERR_ARG;
-  if (max_ksplit < 1 || max_ksplit > 8) return GSS_ERR_ARG;
-  g_max_nw = max_waves;
-  g_ft = features_per_wg / 16;
-  g_max_ksplit = max_ksplit;
-  return GSS_OK;
 }

@@ -1,14 +1,18 @@
-"""The self-speculative round on one MI355X: GLM decoder forward over a paged KV cache through the C-ABI kernels,
+"""The self-spec round on one MI355X: GLM decoder forward over a paged KV cache through the C-ABI kernels,
 with every round-to-round quantity (committed lengths, boundary tokens, accept lengths) resident on the device so a
 whole round is captured once as a HIP graph and replayed.
 
-Per layer of a window forward (rows = bs * W):
-    gss_rmsnorm / gss_add_rmsnorm   input norm, or (residual + post-norm) fused with the next norm
-    qkv = x @ Wqkv^T                hipBLASLt through torch.mm (fused q|k|v projection)
-    gss_rope_stage                  rotate q, k; stage the window K/V (not yet in the cache)
-    gss_draft_attn / gss_verify_attn   paged prefix + window, draft or verify mask
-    o_proj, gate_up, down           hipBLASLt
-    gss_silu_mul                    SwiGLU
+Per layer of a window forward (rows = bs * W, any count: the GEMMs run rows beyond 64 in 64-row slabs with the same
+arithmetic, so every row is computed the same way at every batch size):
+    gss_gemm_rope_stage             fused q|k|v projection, RoPE on q and k, window K/V staged (not yet in the cache)
+    gss_draft_attn / gss_verify_attn   paged prefix + window, draft or verify mask, under the decoder's attention plan
+    gss_gemm_parts (o_proj)         fp32 k-split partial sums
+    gss_add_rmsnorm_parts           residual + post-attention sandwich norm + the MLP input norm (or, at <= 12 rows,
+                                    the same norm inside the gate_up GEMM's prologue)
+    gss_gemm_swiglu                 gate_up projection with the SwiGLU epilogue
+    gss_gemm_parts (down)           fp32 k-split partial sums
+    gss_add_rmsnorm_parts           residual + post-MLP norm + the next layer's input norm
+The prefill (one long prompt) runs its GEMMs through torch.mm; every decode forward runs on the kernels above.
 A round (the serving full-draft round, patches/sglang/.../selfspec_diffusion_worker.py:660-961):
     draft forward [x0 | MASK x B] -> gss_argmax_accept (argmax only) -> gss_kv_commit of row 0 (x0)
     verify forward [a0, d_1..d_B] -> gss_argmax_accept (argmax + accept + bonus) -> gss_kv_commit of acc+1 rows
@@ -55,10 +59,8 @@ class GssEngine:
     """Weights, paged KV pool and kernels for up to ``max_bs`` sequences of up to ``max_len`` tokens each."""
 
     def __init__(self, cfg: GlmTextConfig, weights: Dict[str, torch.Tensor], *, max_bs: int, max_len: int,
-                 device="cuda", page_seed: int = 0, max_win: int = 48, gemm: str = "gss"):
+                 device="cuda", page_seed: int = 0, max_win: int = 48):
         self.cfg = cfg
-        # "gss": the batch-invariant skinny GEMMs (rows <= 64); "torch": hipBLASLt through torch.mm everywhere
-        self.gemm_impl = gemm
         # the GEMM prologue norm is bit-identical only to an unsplit GEMM; the decode path normalizes in the GEMM
         # epilogues instead, for every row count (0 = the prologue path is off)
         self.fuse_norm_rows = 0
@@ -109,14 +111,31 @@ class GssEngine:
                                                                  max_win, max_len)), dtype=torch.uint8, device=dev)
         self.ws_arg = torch.zeros(K.argmax_workspace_bytes(max_bs, max_win, cfg.vocab), dtype=torch.uint8, device=dev)
         self.ws_commit = torch.zeros(K.commit_workspace_bytes(max_bs), dtype=torch.uint8, device=dev)
-        rows = min(64, max_bs * max_win)
+        rows = max_bs * max_win
         shapes = [(cfg.qkv_dim, cfg.hidden), (cfg.hidden, cfg.n_heads * cfg.head_dim), (2 * cfg.ffn, cfg.hidden),
                   (cfg.hidden, cfg.ffn), (cfg.vocab, cfg.hidden)]
         self.ws_gemm = torch.zeros(max(K.gemm_workspace_bytes(rows, n, kd) for n, kd in shapes), dtype=torch.uint8,
                                    device=dev)
         self._bufs: Dict[Tuple[int, int], _Bufs] = {}
+        self._retired_ws: List[torch.Tensor] = []
 
     # ------------------------------------------------------------------------------------------ primitives ------
+    def attn_plan(self, bs: int, max_kv_len: Optional[int] = None, **policy):
+        """The attention plan of a bs-sequence batch over this cache (the library default unless policy overrides
+        target_wgs / min_tiles / wide_min)."""
+        return K.attn_plan(bs, self.cfg.n_kv_heads, self.max_len if max_kv_len is None else max_kv_len, **policy)
+
+    def _attn_ws(self, bs: int, W: int, plan) -> torch.Tensor:
+        """The attention workspace, grown (outside graph capture: every shape runs eagerly before it is captured)
+        when a plan needs more than the engine's default."""
+        c = self.cfg
+        need = K.attn_workspace_bytes(bs, c.n_heads, c.n_kv_heads, c.head_dim, W, plan)
+        if need > self.ws_attn.numel():
+            # graphs captured earlier still hold the old buffer's address: it is kept, never freed
+            self._retired_ws.append(self.ws_attn)
+            self.ws_attn = torch.zeros(need, dtype=torch.uint8, device=self.device)
+        return self.ws_attn
+
     def bufs(self, bs: int, W: int) -> _Bufs:
         key = (bs, W)
         if key not in self._bufs:
@@ -128,21 +147,22 @@ class GssEngine:
     def forward(self, b: _Bufs, *, ids: Optional[torch.Tensor] = None, emb: Optional[torch.Tensor] = None,
                 n_causal: Optional[int], seq_lens: Optional[torch.Tensor] = None,
                 page_table: Optional[torch.Tensor] = None, pos_delta: Optional[torch.Tensor] = None,
-                max_kv_len: Optional[int] = None, logits_f32: bool = False) -> torch.Tensor:
+                max_kv_len: Optional[int] = None, attn_plan=None, logits_f32: bool = False) -> torch.Tensor:
         """One window forward of all layers. ``ids`` int32/int64 [bs, W] or ``emb`` [bs*W, H]; n_causal None =
-        verify mask. The window's K/V is left in b.k_win / b.v_win (not committed). Returns logits [bs, W, V] (bf16;
+        verify mask. The window's K/V is left in b.k_win / b.v_win (not committed). ``attn_plan``: the attention
+        plan (default: the library's for bs sequences of capacity max_kv_len). Returns logits [bs, W, V] (bf16;
         fp32 with ``logits_f32``: the LM head's sums before their bf16 rounding, for the sampled round)."""
         c = self.cfg
         bs, W = b.bs, b.W
         b.want_f32 = logits_f32
         sl = self.seq_lens[:bs] if seq_lens is None else seq_lens
         pt = self.page_table[:bs] if page_table is None else page_table
-        mkl = self.max_len if max_kv_len is None else max_kv_len
-        own = self.gemm_impl == "gss" and bs * W <= 64
+        plan = self.attn_plan(bs, max_kv_len) if attn_plan is None else attn_plan
+        self._attn_ws(bs, W, plan)
         # the GEMM-prologue norm path (off by default: it would not match the split-K epilogue path bit for bit)
-        fused = own and bs * W <= self.fuse_norm_rows and c.hidden % 512 == 0 and c.hidden <= 1536
-        if logits_f32 and (not own or fused):
-            raise NotImplementedError("fp32 logits are produced by the decode GEMM path (bs * W <= 64, unfused norms)")
+        fused = bs * W <= min(64, self.fuse_norm_rows) and c.hidden % 512 == 0 and c.hidden <= 1536
+        if logits_f32 and fused:
+            raise NotImplementedError("fp32 logits are produced by the unfused-norm decode path")
         if emb is None and ids.dtype == torch.int32 and ids.is_contiguous() and not fused:
             K.embed_rmsnorm(self.embed, ids, self.n_in[0], b.h, b.x, c.rms_eps)   # lookup + first input norm
         else:
@@ -151,27 +171,11 @@ class GssEngine:
             else:
                 torch.index_select(self.embed, 0, ids.reshape(-1), out=b.h)
             if fused:
-                return self._forward_fused(b, n_causal, sl, pt, pos_delta, mkl)
+                return self._forward_fused(b, n_causal, sl, pt, pos_delta, plan)
             K.rmsnorm(b.h, self.n_in[0], b.x, c.rms_eps)
-        if own:
-            return self._forward_own(b, n_causal, sl, pt, pos_delta, mkl)
-        # more than 64 rows (or gemm="torch"): hipBLASLt GEMMs and the separate norm kernels
-        for l in range(c.n_layers):
-            torch.mm(b.x, self.wqkv[l].t(), out=b.qkv)
-            K.rope_stage(b.qkv, sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], pos_delta=pos_delta,
-                         rot_dim=c.rot_dim)
-            K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
-                               n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
-            torch.mm(b.o.view(bs * W, -1), self.wo[l].t(), out=b.a)
-            K.add_rmsnorm(b.a, self.n_psa[l], b.h, self.n_pa[l], b.x, c.rms_eps)
-            self._swiglu_torch(b.x, self.wgu[l], b.gu, b.act)
-            torch.mm(b.act, self.wdown[l].t(), out=b.a)
-            nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
-            K.add_rmsnorm(b.a, self.n_pm[l], b.h, nxt, b.x, c.rms_eps)
-        torch.mm(b.x, self.lm_head.t(), out=b.logits)
-        return b.logits.view(bs, W, c.vocab)
+        return self._forward_own(b, n_causal, sl, pt, pos_delta, plan)
 
-    def _forward_own(self, b: _Bufs, n_causal, sl, pt, pos_delta, mkl) -> torch.Tensor:
+    def _forward_own(self, b: _Bufs, n_causal, sl, pt, pos_delta, plan) -> torch.Tensor:
         """Decode forward on the batch-invariant GEMMs (b.x already holds the first input norm). Per layer:
         [qkv + RoPE + staging], attention (+ split merge), o_proj, residual norm, [gate_up + SwiGLU], down,
         residual norm (the norms inside the o_proj / down GEMM epilogues when post_norm is set; the post-attention
@@ -184,7 +188,7 @@ class GssEngine:
             K.gemm_rope_stage(b.x, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], rot_dim=c.rot_dim,
                               pos_delta=pos_delta, workspace=ws)
             K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
-                               n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
+                               n_causal=n_causal, scale=self.scale, plan=plan, workspace=self.ws_attn)
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
             if self.post_norm:
                 K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a, workspace=ws,
@@ -225,7 +229,7 @@ class GssEngine:
         K.gemm(b.x, self.lm_head, b.logits, workspace=ws)
         return b.logits.view(bs, W, c.vocab)
 
-    def _forward_fused(self, b: _Bufs, n_causal, sl, pt, pos_delta, mkl) -> torch.Tensor:
+    def _forward_fused(self, b: _Bufs, n_causal, sl, pt, pos_delta, plan) -> torch.Tensor:
         """Decode forward with the sandwich norms folded into the GEMM prologues: per layer
         [norm + qkv + RoPE], attention (+ split merge), o_proj, [norm + gate_up + SwiGLU], down."""
         c = self.cfg
@@ -239,7 +243,7 @@ class GssEngine:
                               pro=dict(a=prev, h_in=h_a, h_out=h_b, w_post=self.n_pm[l - 1] if prev is not None else None,
                                        w_next=self.n_in[l], eps=eps))
             K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
-                               n_causal=n_causal, scale=self.scale, max_kv_len=mkl, workspace=self.ws_attn)
+                               n_causal=n_causal, scale=self.scale, plan=plan, workspace=self.ws_attn)
             K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a)
             K.gemm_swiglu(None, self.wgu[l], b.act,
                           pro=dict(a=b.a, h_in=h_b, h_out=h_a, w_post=self.n_psa[l], w_next=self.n_pa[l], eps=eps))
@@ -293,6 +297,8 @@ class GssEngine:
         starts = torch.arange(0, P, chunk, dtype=torch.int32, device=dev)
         lens = torch.zeros(1, dtype=torch.int32, device=dev)
         pos3 = None if positions is None else positions.to(device=dev, dtype=torch.int32).contiguous()
+        plan = self.attn_plan(1)
+        ws = self._attn_ws(1, min(chunk, P), plan)
         K.rmsnorm(h, self.n_in[0], x, c.rms_eps)
         for l in range(c.n_layers):
             torch.mm(x, self.wqkv[l].t(), out=qkv)
@@ -307,8 +313,7 @@ class GssEngine:
                 n = min(chunk, P - s0)
                 K.window_attention(q[:, s0:s0 + n].contiguous(), self.k_pages[l], self.v_pages[l], pt,
                                    starts[i:i + 1], kw[0, :, s0:s0 + n].contiguous(), vw[0, :, s0:s0 + n].contiguous(),
-                                   o[:, s0:s0 + n], n_causal=None, scale=self.scale, max_kv_len=self.max_len,
-                                   workspace=self.ws_attn)
+                                   o[:, s0:s0 + n], n_causal=None, scale=self.scale, plan=plan, workspace=ws)
             torch.mm(o.view(P, -1), self.wo[l].t(), out=a)
             K.add_rmsnorm(a, self.n_psa[l], h, self.n_pa[l], x, c.rms_eps)
             gu = torch.empty(P, 2 * c.ffn, dtype=bf, device=dev)
@@ -343,11 +348,22 @@ class RoundState:
 
 
 class SelfSpecDecoder:
-    """The full-draft self-spec round and the AR step over a GssEngine, device resident and graph-capturable."""
+    """The full-draft self-spec round and the AR step over a GssEngine, device resident and graph-capturable.
+
+    The decoder owns the engine's sequence slots [slot0, slot0 + bs) (their lengths and page-table rows). Its
+    attention runs under ``attn_plan`` (default: the library plan for bs sequences); a decoder given the plan of a
+    larger batch computes every row exactly as that batch does, so one sequence decoded alone reproduces its rows of
+    the batched decode bit for bit."""
 
     def __init__(self, eng: GssEngine, bd: int, mask_id: int, bs: int = 1, max_rounds: int = 4096,
-                 softmax_rule: bool = False):
+                 softmax_rule: bool = False, slot0: int = 0, attn_plan=None):
         self.eng, self.bd, self.mask_id, self.bs = eng, bd, mask_id, bs
+        if slot0 < 0 or slot0 + bs > eng.max_bs:
+            raise ValueError(f"slots [{slot0}, {slot0 + bs}) exceed the engine's {eng.max_bs}")
+        self.slot0 = slot0
+        self.sl = eng.seq_lens[slot0:slot0 + bs]
+        self.pt = eng.page_table[slot0:slot0 + bs]
+        self.plan = eng.attn_plan(bs) if attn_plan is None else attn_plan
         # greedy rule for rows holding a NaN or +inf: the serving worker's raw argmax (NaN as the maximum), or the
         # HF path's argmax of the fp32 softmax (index 0) with the raw bonus row (src/fast_sampling.py:572-575)
         self.f_draft = K.ARGMAX_SOFTMAX if softmax_rule else 0
@@ -386,9 +402,9 @@ class SelfSpecDecoder:
         e, s = self.eng, self.st
         if self.bs > 1:
             s.win[:, 0].copy_(s.x0)
-        lg = e.forward(self.draft_b, ids=s.win, n_causal=1, pos_delta=self.pos_delta)
+        lg = self._fwd(self.draft_b, s.win, n_causal=1)
         e.argmax(lg, s.am, flags=self.f_draft)                              # a0, d_1..d_B
-        e.commit(self.draft_b, n_add=1)                                     # x0's K/V (causal row 0): S += 1
+        self._commit(self.draft_b, n_add=1)                                 # x0's K/V (causal row 0): S += 1
         if after_draft is not None:
             after_draft()
         self._verify()
@@ -401,26 +417,33 @@ class SelfSpecDecoder:
         e, s = self.eng, self.st
         if self.r0_b is None:
             self.r0_b = e.bufs(self.bs, self.bd)
-        lg = e.forward(self.r0_b, ids=self.r0_ids, n_causal=0, pos_delta=self.pos_delta)
+        lg = self._fwd(self.r0_b, self.r0_ids, n_causal=0)
         e.argmax(lg, self.r0_am, flags=self.f_draft)
         s.am[:, 0].copy_(s.x0)
         s.am[:, 1:].copy_(self.r0_am)
         self._verify()
 
+    def _fwd(self, b, ids, n_causal, **kw):
+        return self.eng.forward(b, ids=ids, n_causal=n_causal, pos_delta=self.pos_delta, seq_lens=self.sl,
+                                page_table=self.pt, attn_plan=self.plan, **kw)
+
+    def _commit(self, b, **kw):
+        self.eng.commit(b, seq_lens=self.sl, page_table=self.pt, **kw)
+
     def _verify(self):
         e, s = self.eng, self.st
-        lg = e.forward(self.verify_b, ids=s.am, n_causal=None, pos_delta=self.pos_delta)
+        lg = self._fwd(self.verify_b, s.am, n_causal=None)
         e.argmax(lg, s.tgt, window=s.am, accept_len=s.acc, next_x0=s.x0, packed=s.packed, flags=self.f_verify)
-        e.commit(self.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)       # a0, d_1..d_acc: S += acc + 1
+        self._commit(self.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)   # a0, d_1..d_acc: S += acc + 1
         # the log index is clamped on the device, so rounds beyond the log's capacity rewrite its last row
         K.log_append(s.ctr, [(s.packed, s.log), (s.am, self.log_am), (s.tgt, self.log_tgt)])
 
     def ar_step(self):
         e = self.eng
-        lg = e.forward(self.ar_b, ids=self.ar_ids, n_causal=None, pos_delta=self.pos_delta)
+        lg = self._fwd(self.ar_b, self.ar_ids, n_causal=None)
         # a one-row window: accept length 0, so next_x0 = the argmax itself (written over the input token)
         e.argmax(lg, self.ar_tgt, window=self.ar_ids, next_x0=self.st.x0)
-        e.commit(self.ar_b, n_add=1)
+        self._commit(self.ar_b, n_add=1)
         K.log_append(self.ar_ctr, [(self.ar_tgt.view(self.bs), self.ar_log)])
 
     def capture(self):

@@ -5,12 +5,10 @@ from typing import Optional
 
 import torch
 
-from ._lib import NormEpilogue, NormPrologue, Penalties, check, lib
+from ._lib import AttnPlan, NormEpilogue, NormPrologue, Penalties, check, lib
 
 PAGE = 16
-# the attention kernels' library defaults (gss_attn_set_split_policy, gss_attn_set_wide_min)
-ATTN_POLICY = (896, 4)
-ATTN_WIDE_MIN = 16
+ATTN_ROWGROUP, ATTN_WIDE = 0, 1
 
 
 def _stream():
@@ -32,9 +30,29 @@ def _need(t: torch.Tensor, dtype, name: str, shape=None):
         raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
 
 
-def attn_workspace_bytes(bs, Hq, Hkv, D, W, max_kv_len) -> int:
+_PLANS = {}
+
+
+def attn_plan(bs: int, Hkv: int, max_kv_len: int, *, target_wgs: int = 0, min_tiles: int = 0,
+              wide_min: int = 0) -> AttnPlan:
+    """The attention plan (kernel + key partition) of a batch shape (gss_attn_make_plan; zeros = the defaults).
+    Plans are values: two calls with the same arguments return equal plans."""
+    key = (bs, Hkv, max_kv_len, target_wgs, min_tiles, wide_min)
+    if key not in _PLANS:
+        plan = AttnPlan()
+        check(lib().gss_attn_make_plan(bs, Hkv, max_kv_len, target_wgs, min_tiles, wide_min, ctypes.byref(plan)),
+              "gss_attn_make_plan")
+        _PLANS[key] = plan
+    return _PLANS[key]
+
+
+def attn_workspace_bytes(bs, Hq, Hkv, D, W, plan) -> int:
+    """Workspace of an attention call; ``plan`` is an AttnPlan or a capacity (the default plan of that capacity)."""
+    if not isinstance(plan, AttnPlan):
+        plan = attn_plan(bs, Hkv, int(plan))
     n = ctypes.c_size_t(0)
-    check(lib().gss_attn_workspace_size(bs, Hq, Hkv, D, W, max_kv_len, ctypes.byref(n)), "gss_attn_workspace_size")
+    check(lib().gss_attn_workspace_size(bs, Hq, Hkv, D, W, ctypes.byref(plan), ctypes.byref(n)),
+          "gss_attn_workspace_size")
     return n.value
 
 
@@ -51,10 +69,12 @@ def commit_workspace_bytes(bs) -> int:
 
 
 def window_attention(q, k_pages, v_pages, page_table, prefix_len, k_win, v_win, out, *, n_causal: Optional[int],
-                     scale: float, max_kv_len: int, workspace: Optional[torch.Tensor], prefix_extra: int = 0):
+                     scale: float, max_kv_len: Optional[int] = None, plan: Optional[AttnPlan] = None,
+                     workspace: Optional[torch.Tensor], prefix_extra: int = 0):
     """Draft (n_causal given) or verify (n_causal None) attention. Shapes: q/out [bs, W, Hq, D] bf16,
     k_pages [n_pages, Hkv, 16, D], v_pages [n_pages, Hkv, D, 16], page_table int32 [bs, P], prefix_len int32 [bs],
-    k_win/v_win [bs, W, Hkv, D]."""
+    k_win/v_win [bs, W, Hkv, D]. ``plan`` (AttnPlan) fixes the kernel and key partition; without one, the default
+    plan of (bs, Hkv, max_kv_len)."""
     bs, W, Hq, D = q.shape
     n_pages, Hkv = k_pages.shape[0], k_pages.shape[1]
     _need(q, torch.bfloat16, "q")
@@ -67,16 +87,20 @@ def window_attention(q, k_pages, v_pages, page_table, prefix_len, k_win, v_win, 
     _need(prefix_len, torch.int32, "prefix_len", (bs,))
     if page_table.shape[0] != bs:
         raise ValueError("page_table rows != batch")
-    if max_kv_len > page_table.shape[1] * PAGE:
-        raise ValueError("max_kv_len exceeds what the page table addresses")
-    need = attn_workspace_bytes(bs, Hq, Hkv, D, W, max_kv_len)
+    if plan is None:
+        if max_kv_len is None:
+            raise ValueError("window_attention needs a plan or a capacity (max_kv_len)")
+        plan = attn_plan(bs, Hkv, int(max_kv_len))
+    if plan.max_kv_len > page_table.shape[1] * PAGE:
+        raise ValueError("the plan's capacity exceeds what the page table addresses")
+    need = attn_workspace_bytes(bs, Hq, Hkv, D, W, plan)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     if need > ws_bytes:
         raise ValueError(f"attention workspace {ws_bytes} B < {need} B")
     L = lib()
     common = (_ptr(q), _ptr(k_pages), _ptr(v_pages), _ptr(page_table), page_table.shape[1], _ptr(prefix_len),
               prefix_extra, _ptr(k_win), _ptr(v_win), _ptr(out), bs, W)
-    tail = (Hq, Hkv, D, PAGE, float(scale), int(max_kv_len), _ptr(workspace), ws_bytes, _stream())
+    tail = (Hq, Hkv, D, PAGE, float(scale), ctypes.byref(plan), _ptr(workspace), ws_bytes, _stream())
     if n_causal is None:
         check(L.gss_verify_attn(*common, *tail), "gss_verify_attn")
     else:

@@ -144,7 +144,7 @@ class SampledSelfSpec:
         V = e.cfg.vocab
         if bs > 1:
             s.win[:, 0].copy_(s.x0)
-        lg = e.forward(d.draft_b, ids=s.win, n_causal=1, pos_delta=d.pos_delta, logits_f32=True)
+        lg = d._fwd(d.draft_b, s.win, n_causal=1, logits_f32=True)
         e.argmax(lg, s.am)                                       # the deterministic draft d_1..d_{K-1}
         row0 = lg[:, 0, :]
         self._process(row0, self.a0_cand)
@@ -152,8 +152,8 @@ class SampledSelfSpec:
         self._draw(row0, bs, 1, self.u_a0, self.a0_tok)          # a0 ~ AR's distribution of the token after x0
         s.am[:, 0].copy_(self.a0_tok[:, 0])
         self._cumulate(self.a0_tok, torch.ones_like(self.a0_tok, dtype=torch.bool))
-        e.commit(d.draft_b, n_add=1)
-        lg = e.forward(d.verify_b, ids=s.am, n_causal=None, pos_delta=d.pos_delta, logits_f32=True)
+        d._commit(d.draft_b, n_add=1)
+        lg = d._fwd(d.verify_b, s.am, n_causal=None, logits_f32=True)
         rows = lg.view(bs * Kw, V)
         self._process(rows, s.am)
         self.coins.uniform_().neg_().add_(1.0)                   # (0, 1]
@@ -164,7 +164,7 @@ class SampledSelfSpec:
                       top_p=self.top_p, min_p=self.min_p, cand=s.am, coins=self.coins, uniforms=self.u,
                       sampled=self.sampled, target=s.tgt, accept_len=s.acc, next_x0=s.x0, packed=s.packed,
                       workspace=self.ws)
-        e.commit(d.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)
+        d._commit(d.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)
         valid = torch.arange(Kw, device=s.acc.device)[None, :] <= s.acc[:, None]
         self._cumulate(s.tgt, valid)
         K.log_append(s.ctr, [(s.packed, s.log), (s.am, d.log_am), (s.tgt, d.log_tgt)])
@@ -172,12 +172,12 @@ class SampledSelfSpec:
     def ar_step(self):
         """One sampled AR decode step with the same processing (the reference distribution of the round)."""
         d, e = self.dec, self.dec.eng
-        lg = e.forward(d.ar_b, ids=d.ar_ids, n_causal=None, pos_delta=d.pos_delta, logits_f32=True)
+        lg = d._fwd(d.ar_b, d.ar_ids, n_causal=None, logits_f32=True)
         row = lg[:, 0, :]
         self._process(row, self.ar_cand)
         self.ar_u.uniform_()
         self._draw(row, d.bs, 1, self.ar_u, self.ar_tok)
-        e.commit(d.ar_b, n_add=1)
+        d._commit(d.ar_b, n_add=1)
         d.st.x0.copy_(self.ar_tok[:, 0])
         self._cumulate(self.ar_tok, torch.ones_like(self.ar_tok, dtype=torch.bool))
         K.log_append(d.ar_ctr, [(self.ar_tok.view(d.bs), d.ar_log)])

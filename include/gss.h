@@ -64,37 +64,46 @@ const char* gss_status_string(int status);
  *                             n_causal = 1 is the serving draft [x0 | MASK x B] and natcache rounds >= 1;
  *                             n_causal = 0 is natcache round 0 and the block-diffusion sampler's full block.
  *   verify (gss_verify_attn): row w sees window rows 0..w (causal, bottom-right aligned).
- * scale multiplies q.k (1/sqrt(D) for GLM). max_kv_len is the cache capacity: every L must be <= max_kv_len. It
- * and bs * Hkv (with the split policy) fix how the keys are partitioned, so calls with different W or L on the same
- * cache and batch size combine every key in the same order (a verify row equals the AR step of the same token bit
- * for bit; rows of different batch sizes agree bit for bit whenever their plans coincide). The
- * workspace holds gss_attn_workspace_size(...) bytes (no zeroing needed). Supported: D in {64, 128}, page = 16,
- * 1 <= W <= 64, Hq % Hkv == 0, max_kv_len + 64 <= 256 * 256 * 64 keys.
+ * scale multiplies q.k (1/sqrt(D) for GLM). Supported: D in {64, 128}, page = 16, 1 <= W <= 64, Hq % Hkv == 0.
+ *
+ * The plan (caller-owned, no process-wide state): the kernel and the key partition, 64-token tiles by absolute
+ * position, tiles_per_split of them per split. It fixes the order in which every key is combined, so any two calls
+ * with the same plan compute a query row the same way whatever W, L or the rest of the batch: a verify row equals
+ * the AR step of the same token bit for bit, and a sequence decoded alone with its batch's plan reproduces its rows
+ * of the batched decode bit for bit. Keep one plan while a cache is decoded. L is clamped to
+ * min(plan->max_kv_len, pt_stride * page): keys past the plan's capacity are never read (callers keep every
+ * prefix within it; the splits cover max_kv_len plus a full window of 64). No counterpart in the reference: the
+ * flashinfer planner's split-KV choice (selfspec_fast_attn.py:288-332) is internal to flashinfer.
  */
-int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, int max_kv_len, size_t* bytes);
+enum gss_attn_kernel {
+  GSS_ATTN_ROWGROUP = 0, /* the rows of a split over up to ceil(R / 48) workgroups: fills the chip from few splits */
+  GSS_ATTN_WIDE = 1      /* one workgroup per key split for all rows, tiles through a ring of LDS slots */
+};
 
-/* Split-KV policy of both attention kernels: about target_wgs / (bs * Hkv) key splits per sequence and kv head, each
- * covering at least min_tiles 64-token tiles (defaults 896 and 4; min_tiles <= 256). Process-wide; set it before
- * sizing workspaces, and keep it fixed while a cache is decoded (it is part of the key partition). */
-int gss_attn_set_split_policy(int target_wgs, int min_tiles);
+typedef struct gss_attn_plan {
+  int kernel;          /* gss_attn_kernel */
+  int tiles_per_split; /* 1..256 */
+  int n_split;         /* 1..256 splits; n_split * tiles_per_split * 64 >= max_kv_len + 64 */
+  int max_kv_len;      /* capacity: the longest prefix L a call may see */
+} gss_attn_plan;
 
-/* Kernel choice of both attention entry points: batches with bs * Hkv >= bs_hkv (default 16) run the wide kernel
- * (one workgroup per key split for all query rows, tiles streamed through a ring of LDS slots), smaller ones the
- * row-group kernel (the rows of a split spread over up to ceil(R / 48) workgroups, which fills the chip from few
- * splits). Process-wide
- * and, like the split policy, part of how a batch's keys are combined: keep it fixed while a cache is decoded.
- * No counterpart in the reference (a launch-shape knob of these kernels). */
-int gss_attn_set_wide_min(int bs_hkv);
+/* Fill *plan for a batch of bs sequences: about target_wgs / (bs * Hkv) key splits per sequence and kv head, each
+ * at least min_tiles tiles; the wide kernel when bs * Hkv >= wide_min. Zero takes the default (896, 4, 16). */
+int gss_attn_make_plan(int bs, int Hkv, int max_kv_len, int target_wgs, int min_tiles, int wide_min,
+                       gss_attn_plan* plan);
+
+/* Workspace bytes (split partials; no zeroing needed) of a call with this shape and plan. */
+int gss_attn_workspace_size(int bs, int Hq, int Hkv, int D, int W, const gss_attn_plan* plan, size_t* bytes);
 
 int gss_draft_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table, int pt_stride,
                    const int32_t* prefix_len, int prefix_extra, const void* k_win, const void* v_win, void* out,
-                   int bs, int W, int n_causal, int Hq, int Hkv, int D, int page, float scale, int max_kv_len,
-                   void* workspace, size_t workspace_bytes, gss_stream_t stream);
+                   int bs, int W, int n_causal, int Hq, int Hkv, int D, int page, float scale,
+                   const gss_attn_plan* plan, void* workspace, size_t workspace_bytes, gss_stream_t stream);
 
 int gss_verify_attn(const void* q, const void* k_pages, const void* v_pages, const int32_t* page_table,
                     int pt_stride, const int32_t* prefix_len, int prefix_extra, const void* k_win, const void* v_win,
-                    void* out, int bs, int W, int Hq, int Hkv, int D, int page, float scale, int max_kv_len,
-                    void* workspace, size_t workspace_bytes, gss_stream_t stream);
+                    void* out, int bs, int W, int Hq, int Hkv, int D, int page, float scale,
+                    const gss_attn_plan* plan, void* workspace, size_t workspace_bytes, gss_stream_t stream);
 
 /* ---------------------------------------------------------------- (c) argmax + accept + bonus -------------------
  * Replaces torch.argmax over the verify/draft logits (selfspec_diffusion_worker.py:742; src/fast_sampling.py:545,
@@ -219,8 +228,11 @@ int gss_sample_rows(const float* logits, int64_t ld_row, int bs, int K, int V, i
  * The dense projections of the decoder layer and the LM head (transformers GlmOcrTextAttention q/k/v/o_proj,
  * GlmOcrTextMLP gate_up/down_proj and lm_head, which the reference runs as torch linears through
  * src/fast_sampling.py:89-102). Y[M, N] = X[M, Kd] . W[N, Kd]^T, bf16 operands (row strides in elements, 16-byte
- * aligned), fp32 accumulation, M <= 64, Kd % 32 == 0, N % 16 == 0. A row's result does not depend on M or on the
- * row's position (batch invariant), so speculative verify rows reproduce AR rows bit for bit.
+ * aligned), fp32 accumulation, M <= 65536, Kd % 32 == 0, N % 16 == 0. A row's result does not depend on M or on the
+ * row's position (batch invariant), so speculative verify rows reproduce AR rows bit for bit, at every batch size.
+ * The launch shape (waves per workgroup, k splits, features per workgroup) is a function of (N, Kd) and the
+ * device's CU count only: it is the reduction order, so it is not a setting. The fused prologue and the post-norm
+ * epilogue need every row in one workgroup: M <= 64 with either (GSS_ERR_UNSUPPORTED above).
  * gss_gemm: Y bf16 or fp32. gss_gemm_swiglu: W = gate_up with gate/up rows interleaved (2i = gate_i, 2i+1 = up_i),
  * act[M, F] = up * silu(gate). gss_gemm_rope_stage: W = [Wq; Wk; Wv], output q [bs, W, Hq, D] rotated,
  * window K/V [bs, W, Hkv, D] with K rotated (positions as gss_rope_stage with pos_offset 0).
@@ -241,12 +253,6 @@ typedef struct gss_norm_prologue {
                            sum in part order, as gss_add_rmsnorm_parts computes it), or NULL */
   int n_parts;
 } gss_norm_prologue;
-
-/* Launch-shape policy of the three GEMMs (process-wide): at most max_waves (1..12) waves per workgroup splitting
- * Kd, features_per_wg output features per workgroup (16 or 32; 0 = 16 unless N > 32768), and at most max_ksplit
- * (1..8) k splits over workgroups for shapes with few column tiles and at least 64 k-steps per split (default 2).
- * The split count is part of the reduction order: keep the policy fixed while a cache is decoded. */
-int gss_gemm_set_policy(int max_waves, int features_per_wg, int max_ksplit);
 
 /* Norm epilogue of gss_gemm (the sandwich norm after o_proj and after the MLP down projection,
  * modeling_glm_ocr.py:263-310): once Y = X W^T is written (bf16, ldy == N, N = hidden size), every row gets

@@ -110,20 +110,24 @@ def natcache_generate(model: OracleDecoder, prefix_emb: torch.Tensor, bd: int, m
 
 
 def fulldraft_round(model: OracleDecoder, cache: KVCache, S: int, x0: int, bd: int, mask_id: int,
-                    pos_offset: int = 0, trace: Optional[list] = None):
+                    pos_offset: int = 0, trace: Optional[list] = None, verify_window: Optional[List[int]] = None):
     """One serving full-draft round (patches/sglang/.../selfspec_diffusion_worker.py:660-961 with
     selfspec_fast_commit.py:108-147), K = bd + 1 rows per forward, AR-aligned positions (SELFSPEC_POS_OFFSET=0):
       draft  [x0 | MASK x bd] at positions S+pos_offset.. (x0 row causal, mask rows bidirectional); am = argmax.
       x0's K/V (draft row 0, causal, exact) is committed: S += 1.
       verify [a0, d_1..d_bd] = am at positions S.. (causal); t = argmax; acc = leading matches t_r == d_{r+1}.
       commit T = [a0, t_0..t_acc]; keep verify K/V rows 0..acc: S += acc + 1; x0 = t_acc.
-    ``cache`` holds exactly S committed positions on entry and S' on return. Returns (S', x0', T, acc, record)."""
+    ``cache`` holds exactly S committed positions on entry and S' on return. Returns (S', x0', T, acc, record).
+    ``verify_window`` (K ids) replaces the draft's own argmax as the verify window: the replay of another
+    implementation's round from the same state (its draft argmax may differ from this one's at near ties)."""
     K = bd + 1
     ids = torch.tensor([x0] + [mask_id] * bd)
     cache.truncate(S)
     dl = model.logits(model.forward(model.embed(ids), torch.arange(S, S + K) + pos_offset, cache,
                                     window_mask(S, K, 1)))
     am = dl.float().argmax(-1)                                           # [K] = a0, d_1..d_bd
+    if verify_window is not None:
+        am = torch.as_tensor(list(verify_window), dtype=torch.long)
     cache.truncate(S + 1)                                                # x0 committed from draft row 0
     S1 = S + 1
     vl = model.logits(model.forward(model.embed(am), torch.arange(S1, S1 + K) + pos_offset, cache,

@@ -43,9 +43,12 @@ def test_host_side_queries_and_status_strings():
     assert L.gss_argmax_workspace_size(1, 17, 131073, ctypes.byref(n)) == UNSUPPORTED
     assert L.gss_argmax_workspace_size(1, 65, 100, ctypes.byref(n)) == UNSUPPORTED
     assert L.gss_argmax_workspace_size(0, 17, 100, ctypes.byref(n)) == ARG
-    assert L.gss_attn_workspace_size(1, 16, 2, 128, 17, 8192, ctypes.byref(n)) == OK and n.value > 0
-    assert L.gss_attn_workspace_size(1, 16, 3, 128, 17, 8192, ctypes.byref(n)) == UNSUPPORTED   # Hq % Hkv
-    assert L.gss_attn_workspace_size(1, 16, 2, 96, 17, 8192, ctypes.byref(n)) == UNSUPPORTED    # head dim
+    plan = _lib.AttnPlan()
+    assert L.gss_attn_make_plan(1, 2, 8192, 0, 0, 0, ctypes.byref(plan)) == OK
+    assert L.gss_attn_workspace_size(1, 16, 2, 128, 17, ctypes.byref(plan), ctypes.byref(n)) == OK and n.value > 0
+    assert L.gss_attn_workspace_size(1, 16, 3, 128, 17, ctypes.byref(plan), ctypes.byref(n)) == UNSUPPORTED  # Hq % Hkv
+    assert L.gss_attn_workspace_size(1, 16, 2, 96, 17, ctypes.byref(plan), ctypes.byref(n)) == UNSUPPORTED   # head dim
+    assert L.gss_attn_workspace_size(1, 16, 2, 128, 17, None, ctypes.byref(n)) == ARG
     assert L.gss_kv_commit_workspace_size(4, ctypes.byref(n)) == OK
     # unmask: the same counters + chunk (max, index, sum) of ceil(V / 4096) chunks per row, 16 B each
     assert L.gss_unmask_workspace_size(2, 32, 59392, ctypes.byref(n)) == OK
@@ -57,19 +60,25 @@ def test_entry_points_reject_bad_arguments_before_launch():
     L = _lib.lib()
     null = None
     # null pointers
+    plan = _lib.AttnPlan()
+    assert L.gss_attn_make_plan(1, 2, 8192, 0, 0, 0, ctypes.byref(plan)) == OK
+    pp = ctypes.byref(plan)
     assert L.gss_draft_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 17, 1, 16, 2, 128, 16, 0.1,
-                            8192, null, 0, null) == ARG
+                            pp, null, 0, null) == ARG
     assert L.gss_argmax_accept(null, 0, 100, 1, 1, 100, 0, null, null, null, null, null, null, 0, null) == ARG
     assert L.gss_unmask_step(null, 0, 100, 1, 4, 100, null, 7, 0.9, null, null, null, null, null, null, 0, null) == ARG
     # unsupported page size / window wider than a tile: rejected before pointers are looked at
     assert L.gss_verify_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 17, 16, 2, 128, 32, 0.1,
-                             8192, null, 0, null) == UNSUPPORTED
+                             pp, null, 0, null) == UNSUPPORTED
     assert L.gss_verify_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 65, 16, 2, 128, 16, 0.1,
-                             8192, null, 0, null) == UNSUPPORTED
-    assert L.gss_gemm_set_policy(0, 16, 1) == ARG
-    assert L.gss_gemm_set_policy(12, 16, 9) == ARG
-    assert L.gss_attn_set_split_policy(0, 2) == ARG
-    assert L.gss_attn_set_wide_min(0) == ARG
+                             pp, null, 0, null) == UNSUPPORTED
+    # a missing plan, or one whose splits do not cover its capacity plus a window, is rejected
+    bad = _lib.AttnPlan(1, 4, 2, 8192)
+    for p in (None, ctypes.byref(bad)):
+        assert L.gss_verify_attn(null, null, null, null, 1, null, 0, null, null, null, 1, 17, 16, 2, 128, 16, 0.1,
+                                 p, null, 0, null) == ARG
+    assert L.gss_attn_make_plan(1, 2, 8192, -1, 0, 0, pp) == ARG
+    assert L.gss_attn_make_plan(1, 2, 8192, 0, 257, 0, pp) == ARG
     # the parts norm is built for 1..4 fp32 parts (gss_gemm_parts writes at most 2); dummy aligned pointers are
     # never dereferenced on a rejected call
     fake = ctypes.c_void_p(1 << 20)
@@ -133,24 +142,40 @@ def test_dropin_rejects_unimplemented_modes_and_cpu_models():
 
 
 def test_gemm_workspace_sizes_follow_the_k_split():
-    """With k splits allowed, split-K partials only for shapes whose column tiles leave CUs idle and whose splits keep
-    at least 64 k-steps (the down projection of the 1536-hidden decoder); the counters' block is always there."""
+    """Split-K partials only for shapes whose column tiles leave CUs idle and whose splits keep at least 64 k-steps
+    (the down projection of the 1536-hidden decoder, 2 splits); the counters' block is always there. The split is a
+    function of the weight shape only, so it scales with M and nothing else."""
     L = _lib.lib()
     n = ctypes.c_size_t(0)
     sizes = {}
-    assert L.gss_gemm_set_policy(12, 0, 1) == OK
-    assert L.gss_gemm_workspace_size(17, 1536, 4608, ctypes.byref(n)) == OK
-    unsplit = n.value                                        # no k split allowed
-    assert L.gss_gemm_set_policy(12, 0, 8) == OK
-    try:
+    for M in (17, 544):
         for N, Kd in [(2560, 1536), (1536, 2048), (9216, 1536), (1536, 4608), (59392, 1536)]:
-            assert L.gss_gemm_workspace_size(17, N, Kd, ctypes.byref(n)) == OK
-            sizes[(N, Kd)] = n.value
-    finally:
-        assert L.gss_gemm_set_policy(12, 0, 2) == OK
-    assert unsplit == sizes[(9216, 1536)]
-    ctr = sizes[(9216, 1536)]
-    assert sizes[(59392, 1536)] == ctr                          # many column tiles: unsplit
-    assert sizes[(2560, 1536)] == ctr                          # 48 k-steps: too short to split
-    assert sizes[(1536, 2048)] == ctr                          # 64 k-steps: one split of 64
-    assert sizes[(1536, 4608)] == ctr + 2 * 17 * 1536 * 4      # 144 k-steps, 96 column tiles -> 2 splits
+            assert L.gss_gemm_workspace_size(M, N, Kd, ctypes.byref(n)) == OK
+            sizes[(M, N, Kd)] = n.value
+    ctr = sizes[(17, 9216, 1536)]
+    for M in (17, 544):
+        assert sizes[(M, 9216, 1536)] == ctr
+        assert sizes[(M, 59392, 1536)] == ctr                       # many column tiles: unsplit
+        assert sizes[(M, 2560, 1536)] == ctr                        # 48 k-steps: too short to split
+        assert sizes[(M, 1536, 2048)] == ctr                        # 64 k-steps: one split of 64
+        assert sizes[(M, 1536, 4608)] == ctr + 2 * M * 1536 * 4     # 144 k-steps, 96 column tiles -> 2 splits
+
+
+def test_attn_plans_are_values_of_their_arguments():
+    """gss_attn_make_plan: the default policy (about 896 / (bs * Hkv) splits of at least 4 tiles; the wide kernel
+    from bs * Hkv = 16), overrides per call, and no process-wide state between calls."""
+    L = _lib.lib()
+
+    def mk(*a):
+        p = _lib.AttnPlan()
+        assert L.gss_attn_make_plan(*a, ctypes.byref(p)) == OK
+        return p.key()
+
+    tiles = (8192 + 64 + 63) // 64  # 129
+    k1 = mk(1, 2, 8192, 0, 0, 0)
+    assert k1 == (0, 4, (tiles + 3) // 4, 8192)
+    k32 = mk(32, 2, 12288, 0, 0, 0)
+    assert k32[0] == 1 and k32[2] * k32[1] * 64 >= 12288 + 64
+    assert mk(1, 2, 8192, 0, 0, 1)[0] == 1                           # wide kernel by override
+    assert mk(1, 2, 8192, 1, 256, 0)[1:3] == (256, 1)                 # one split
+    assert mk(1, 2, 8192, 0, 0, 0) == k1                              # the override left nothing behind

@@ -3,7 +3,8 @@
 Kernel-only workload: 1 sequence, 16 q / 2 kv heads, head_dim 128, committed prefix L in {1K, 4K, 8K, 16K} in
 16-token pages in a shuffled page order, 17 window rows (boundary token + 16 masks), Q/K/V ~ N(0,1)/sqrt(128),
 seed 1; draft mask (row 0 causal, rows 1.. bidirectional) and verify mask (causal). Tolerance: max |err| <=
-1e-2 * max |ref| (bf16 output). Every case runs on both kernels (row-group and wide). Unused cache slots hold NaN, so a read outside the committed prefix would show.
+1e-2 * max |ref| (bf16 output). Every case runs on both kernels (row-group and wide, chosen through the plan).
+Unused cache slots hold NaN, so a read outside the committed prefix would show.
 """
 import numpy as np
 import pytest
@@ -15,19 +16,22 @@ from tests.helpers import ATTN_REL, PAGE, rel_err, shuffled_page_table
 pytestmark = pytest.mark.gpu
 
 
+# plan policy of the current case (the attn_kernel fixture picks the kernel through wide_min)
+_POLICY = {}
+
+
 @pytest.fixture(autouse=True, params=["rowgroup", "wide"])
 def attn_kernel(request):
     """Every case runs through both attention kernels: the row-group kernel (small batches) and the wide kernel
-    (large batches), selected by the bs * Hkv threshold."""
-    from gravityocr_amd._lib import lib
-    from gravityocr_amd.kernels import ATTN_WIDE_MIN
-    assert lib().gss_attn_set_wide_min(1 << 30 if request.param == "rowgroup" else 1) == 0
+    (large batches), chosen by the plan's bs * Hkv threshold."""
+    _POLICY.clear()
+    _POLICY["wide_min"] = 1 << 30 if request.param == "rowgroup" else 1
     yield request.param
-    assert lib().gss_attn_set_wide_min(ATTN_WIDE_MIN) == 0
+    _POLICY.clear()
 
 
 def run_case(dev, Ls, W, n_causal, Hq=16, Hkv=2, D=128, seed=1, max_kv_len=None, prefix_extra=0, verify=False,
-             ws_fill=0):
+             ws_fill=0, plan=None, inputs=None):
     bs = len(Ls)
     g = torch.Generator().manual_seed(seed)
     sc = D ** -0.5
@@ -54,13 +58,19 @@ def run_case(dev, Ls, W, n_causal, Hq=16, Hkv=2, D=128, seed=1, max_kv_len=None,
         nc = W if verify else n_causal
         refs.append(masked_attention(q[b], torch.cat([k, k_win[b]]), torch.cat([v, v_win[b]]),
                                      window_mask(L, W, nc), sc))
-    from gravityocr_amd.kernels import attn_workspace_bytes, window_attention
-    ws = torch.full((max(1, attn_workspace_bytes(bs, Hq, Hkv, D, W, cap)),), ws_fill, dtype=torch.uint8, device=dev)
+    from gravityocr_amd.kernels import attn_plan, attn_workspace_bytes, window_attention
+    if plan is None:
+        plan = attn_plan(bs, Hkv, cap, **_POLICY)
+    ws = torch.full((max(1, attn_workspace_bytes(bs, Hq, Hkv, D, W, plan)),), ws_fill, dtype=torch.uint8,
+                    device=dev)
     out = torch.empty(bs, W, Hq, D, dtype=torch.bfloat16, device=dev)
-    window_attention(q.to(dev), k_pages.to(dev), v_pages.to(dev), torch.as_tensor(pt).to(dev),
-                     torch.tensor(Ls, dtype=torch.int32, device=dev), k_win.to(dev), v_win.to(dev), out,
-                     n_causal=None if verify else n_causal, scale=sc, max_kv_len=cap, workspace=ws,
-                     prefix_extra=prefix_extra)
+    dv = dict(q=q.to(dev), k_pages=k_pages.to(dev), v_pages=v_pages.to(dev), pt=torch.as_tensor(pt).to(dev),
+              k_win=k_win.to(dev), v_win=v_win.to(dev))
+    if inputs is not None:
+        inputs.update(dv)
+    window_attention(dv["q"], dv["k_pages"], dv["v_pages"], dv["pt"], torch.tensor(Ls, dtype=torch.int32, device=dev),
+                     dv["k_win"], dv["v_win"], out, n_causal=None if verify else n_causal, scale=sc, plan=plan,
+                     workspace=ws, prefix_extra=prefix_extra)
     torch.cuda.synchronize()
     out = out.cpu()
     assert torch.isfinite(out.float()).all()
@@ -136,20 +146,30 @@ def test_deterministic(cuda):
 @pytest.mark.parametrize("policy", [(1, 256), (4096, 1), (64, 9)])
 def test_split_policies(cuda, policy):
     """One split (direct output), one tile per split (many partials, one key lane idle), and 9-tile splits (several
-    stages per split, the last one half full)."""
-    from gravityocr_amd._lib import lib
-    from gravityocr_amd.kernels import ATTN_POLICY
+    stages per split, the last one half full), each a plan of its own (no process-wide state)."""
     print(f"policy={policy}", flush=True)
-    assert lib().gss_attn_set_split_policy(*policy) == 0
-    try:
-        run_case(cuda, [5000], 17, 1, seed=21)
-        run_case(cuda, [5000, 17, 700], 17, 1, seed=22, verify=True, max_kv_len=6000)
-    finally:
-        assert lib().gss_attn_set_split_policy(*ATTN_POLICY) == 0
+    _POLICY.update(target_wgs=policy[0], min_tiles=policy[1])
+    run_case(cuda, [5000], 17, 1, seed=21)
+    run_case(cuda, [5000, 17, 700], 17, 1, seed=22, verify=True, max_kv_len=6000)
 
 
-def test_stale_workspace(cuda):
-    """The workspace is shared by calls of every window size, so split slots a call does not use hold leftovers:
-    all-ones bytes (NaN / -inf words) must not leak into the result."""
-    run_case(cuda, [1024], 17, 1, seed=31, max_kv_len=6000, ws_fill=0xFF)
-    run_case(cuda, [300, 4000], 1, 1, seed=32, max_kv_len=6000, ws_fill=0xFF, verify=True)
+def test_batch_plan_reproduces_rows_alone(cuda):
+    """A sequence of a ragged 32-sequence batch, computed alone under the batch's plan, gives its rows of the batched
+    call bit for bit (same kernel, same key partition), for the draft and the verify mask."""
+    from gravityocr_amd.kernels import attn_plan, attn_workspace_bytes, window_attention
+    rng = np.random.default_rng(33)
+    Ls = [int(x) for x in rng.integers(1024, 12289, size=32)]
+    cap = 12288
+    plan = attn_plan(32, 2, cap, **_POLICY)
+    for verify in (False, True):
+        ins = {}
+        out_b, _ = run_case(cuda, Ls, 17, 1, seed=33, max_kv_len=cap, verify=verify, plan=plan, inputs=ins)
+        q, kp, vp, pt, kw, vw = (ins[k] for k in ("q", "k_pages", "v_pages", "pt", "k_win", "v_win"))
+        ws = torch.zeros(max(1, attn_workspace_bytes(1, 16, 2, 128, 17, plan)), dtype=torch.uint8, device=cuda)
+        for b in (0, 7, 31):
+            out = torch.empty(1, 17, 16, 128, dtype=torch.bfloat16, device=cuda)
+            window_attention(q[b:b + 1], kp, vp, pt[b:b + 1], torch.tensor([Ls[b]], dtype=torch.int32, device=cuda),
+                             kw[b:b + 1], vw[b:b + 1], out, n_causal=None if verify else 1, scale=128 ** -0.5,
+                             plan=plan, workspace=ws)
+            torch.cuda.synchronize()
+            assert torch.equal(out[0].cpu(), out_b[b]), (verify, b)

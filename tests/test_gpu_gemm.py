@@ -33,7 +33,9 @@ def test_gemm_parity_and_fp32_out(cuda, M, N, Kd):
     assert torch.equal(y, y32.bfloat16())
 
 
-@pytest.mark.parametrize("M,N,Kd", [(17, 2560, 1536), (17, 1536, 4608), (33, 59392, 1536), (64, 512, 256)])
+@pytest.mark.parametrize("M,N,Kd", [(17, 2560, 1536), (17, 1536, 4608), (33, 59392, 1536), (64, 512, 256),
+                                    (65, 2560, 1536), (544, 9216, 1536), (561, 59392, 1536), (136, 1536, 2048),
+                                    (1056, 96, 64)])
 def test_gemm_batch_invariance(cuda, M, N, Kd):
     from gravityocr_amd.kernels import gemm
     g = torch.Generator().manual_seed(3)
@@ -140,17 +142,9 @@ def test_norm_prologue_equals_unfused(cuda, M):
     assert torch.equal(act, act_ref) and torch.equal(h_out2, h_ref)
 
 
-@pytest.fixture(params=[1, 8], ids=["unsplit", "ksplit"])
-def ksplit_policy(request):
-    """The GEMM policy with k splits off and allowed up to 8 (the default, 2, is restored afterwards)."""
-    from gravityocr_amd._lib import lib
-    assert lib().gss_gemm_set_policy(12, 0, request.param) == 0
-    yield request.param
-    assert lib().gss_gemm_set_policy(12, 0, 2) == 0
-
-
-@pytest.mark.parametrize("M,N,Kd", [(17, 2560, 1536), (1, 1536, 2048), (17, 1536, 4608), (64, 1536, 4608)])
-def test_gemm_split_k_parity_and_invariance(cuda, ksplit_policy, M, N, Kd):
+@pytest.mark.parametrize("M,N,Kd", [(17, 2560, 1536), (1, 1536, 2048), (17, 1536, 4608), (64, 1536, 4608),
+                                    (544, 1536, 4608)])
+def test_gemm_split_k_parity_and_invariance(cuda, M, N, Kd):
     """Split-K keeps fp32-reference parity and batch invariance (a row alone == the same row in a batch)."""
     from gravityocr_amd.kernels import gemm
     g = torch.Generator().manual_seed(M + N + Kd)
@@ -168,7 +162,7 @@ def test_gemm_split_k_parity_and_invariance(cuda, ksplit_policy, M, N, Kd):
 
 @pytest.mark.parametrize("M", [1, 17, 64])
 @pytest.mark.parametrize("N,Kd", [(1536, 2048), (1536, 4608), (512, 704), (2048, 1536)])
-def test_post_norm_epilogue_equals_separate_norm(cuda, ksplit_policy, M, N, Kd):
+def test_post_norm_epilogue_equals_separate_norm(cuda, M, N, Kd):
     """gss_norm_epilogue (h += rmsnorm(Y) * w_post; x = rmsnorm(h) * w_next inside the GEMM) == the plain GEMM followed
     by gss_add_rmsnorm, bit for bit, for split-K (Kd = 4608) and unsplit shapes, 1 to 4 chunks of 8 per lane."""
     from gravityocr_amd.kernels import add_rmsnorm, gemm
@@ -202,7 +196,7 @@ def test_post_norm_epilogue_rejects_other_widths(cuda):
         gemm(x, w, y, workspace=ws, post=dict(h=h, w_post=one, w_next=one, x=xo, eps=1e-5))
 
 
-def test_split_k_shapes_share_one_workspace(cuda, ksplit_policy):
+def test_split_k_shapes_share_one_workspace(cuda):
     """The decoder's GEMM shapes one after another on one workspace (split and unsplit, different tile counts) give
     the results of the same calls on fresh workspaces."""
     from gravityocr_amd.kernels import gemm, gemm_workspace_bytes
@@ -224,7 +218,7 @@ def test_split_k_shapes_share_one_workspace(cuda, ksplit_policy):
 
 
 PARTS_SHAPES = [(17, 1536, 2048), (17, 1536, 4608), (1, 1536, 2048), (1, 1536, 4608), (33, 1536, 2048),
-                (5, 256, 256), (5, 256, 704)]
+                (5, 256, 256), (5, 256, 704), (544, 1536, 2048), (561, 1536, 4608), (100, 256, 704)]
 
 
 @pytest.mark.parametrize("M,N,Kd", PARTS_SHAPES)
@@ -317,3 +311,36 @@ def test_norms_on_parts_equal_unfused(cuda, M):
         gemm_swiglu(None, wgu, act, pro=dict(a_parts=parts, h_in=h, h_out=h_out, w_post=wp, w_next=wn, eps=eps))
         torch.cuda.synchronize()
         assert torch.equal(act, act_ref) and torch.equal(h_out, h_ref)
+
+
+@pytest.mark.parametrize("bs,W", [(4, 17), (32, 17), (32, 33), (8, 9)])
+def test_batched_epilogues_equal_rows_alone(cuda, bs, W):
+    """Windows of more than 64 rows (64-row slabs): the RoPE + staging and SwiGLU epilogues of a batch give, for every
+    sequence, exactly what a one-sequence call gives (positions from each sequence's own length)."""
+    from gravityocr_amd.kernels import gemm_rope_stage, gemm_swiglu
+    from gravityocr_amd.model import SYNTH_1536 as cfg
+    print(f"batched epilogues bs={bs} W={W}", flush=True)
+    g = torch.Generator().manual_seed(bs * 100 + W)
+    Hq, Hkv, D, Kd, F = 16, 2, 128, 1536, 4608
+    x = torch.randn(bs * W, Kd, generator=g).bfloat16().to(cuda)
+    w = (torch.randn((Hq + 2 * Hkv) * D, Kd, generator=g) * 0.02).bfloat16().to(cuda)
+    wgu = (torch.randn(2 * F, Kd, generator=g) * 0.02).bfloat16().to(cuda)
+    sl = torch.randint(0, 12000, (bs,), generator=g, dtype=torch.int32).to(cuda)
+    pd = torch.randint(-50, 50, (bs,), generator=g, dtype=torch.int32).to(cuda)
+    rot = cfg.rot_dim
+    inv = (1.0 / (cfg.rope_theta ** (torch.arange(0, rot, 2).float() / rot))).to(cuda)
+    q = torch.empty(bs, W, Hq, D, dtype=torch.bfloat16, device=cuda)
+    k = torch.empty(bs, W, Hkv, D, dtype=torch.bfloat16, device=cuda)
+    v = torch.empty_like(k)
+    gemm_rope_stage(x, w, sl, inv, q, k, v, rot_dim=rot, pos_delta=pd)
+    act = torch.empty(bs * W, F, dtype=torch.bfloat16, device=cuda)
+    gemm_swiglu(x, wgu, act)
+    for b in sorted({0, bs // 2, bs - 1}):
+        xb = x[b * W:(b + 1) * W].contiguous()
+        q1, k1, v1 = (torch.empty(1, *t.shape[1:], dtype=torch.bfloat16, device=cuda) for t in (q, k, v))
+        gemm_rope_stage(xb, w, sl[b:b + 1], inv, q1, k1, v1, rot_dim=rot, pos_delta=pd[b:b + 1])
+        a1 = torch.empty(W, F, dtype=torch.bfloat16, device=cuda)
+        gemm_swiglu(xb, wgu, a1)
+        torch.cuda.synchronize()
+        assert torch.equal(q1[0], q[b]) and torch.equal(k1[0], k[b]) and torch.equal(v1[0], v[b]), b
+        assert torch.equal(a1, act[b * W:(b + 1) * W]), b

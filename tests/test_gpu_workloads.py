@@ -1,0 +1,256 @@
+"""The two full-size decode workloads on the GPU, on the 16-layer, 1536-hidden GLM decoder (16 q / 2 kv heads,
+head_dim 128, SwiGLU 4608, vocab 59392, bf16, N(0, 0.02) weights, seed 2):
+
+bs = 1 rounds at an 8K prefix (2048 N(0,1) visual embeddings + 6144 ids, prefilled), B = 16, 40 graph-replayed rounds:
+  * the committed ids equal the engine's own AR greedy decode (graph-replayed one-row steps) bit for bit;
+  * one mid-run round, replayed through the fp32 oracle from the same state (the GPU's KV cache, x0 and, for the
+    verify half, the GPU's verify window): draft and verify logits within the bf16 logit tolerance (2e-2), and the
+    oracle's verify argmax equal to the GPU's except where the oracle's own top-2 gap is below twice that;
+  * that round's integer outputs bit-exact against the oracle's integer rules applied to the GPU's logits: targets
+    (first-index argmax of the bf16 rows), accept length (linear chain), packed row, next x0, committed length and
+    the paged-KV slot of every committed row (page_table[pos // 16] * 16 + pos % 16).
+
+32 sequences with ragged prefixes U[1024, 12288] (seed 3) in one shuffled 16-token page pool, B in {8, 16, 32}
+(windows of 9, 17, 33 rows: 288 to 1056 rows per forward, the GEMMs' 64-row slabs), 6 rounds each, both with the
+random model's own drafts and with planted drafts (the AR tokens up to a per-sequence, per-round mismatch drawn
+geometric(0.1), so accept lengths vary between sequences and rounds):
+  * every sequence's committed ids equal its own AR decode; the AR decode of the batch equals, sequence by sequence,
+    a one-sequence AR decode under the batch's attention plan, bit for bit;
+  * every round's committed slots equal the page-table rule for the committed positions, -1 past the accept length.
+The prefix K/V is seeded N(0, 0.8) (the spread of this model's projected K/V) written straight into the pages.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import LOGIT_ABS
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2 * LOGIT_ABS  # a GPU argmax may differ from the fp32 oracle's only where the oracle's top-2 gap is below this
+
+
+@pytest.fixture(scope="module")
+def weights16():
+    from gravityocr_amd.model import SYNTH_1536, synthetic_weights
+    print("drawing the 16-layer decoder's weights", flush=True)
+    return synthetic_weights(SYNTH_1536, 2)
+
+
+def _capture_ar(dec):
+    """One eager AR step (warm-up), then the AR step captured as a graph."""
+    dec.ar_step()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        dec.ar_step()
+    return g
+
+
+# ---------------------------------------------------------------------------------------------- bs = 1 at 8K ----
+def test_bs1_rounds_at_8k_prefix(cuda, weights16):
+    from gravityocr_amd.engine import GssEngine, SelfSpecDecoder
+    from gravityocr_amd.model import SYNTH_1536 as cfg, synthetic_prompt
+    from oracle.decoder import DecoderConfig, KVCache, OracleDecoder
+    from oracle.integer import accept_chain, argmax_first, page_slot
+    from oracle.rounds import fulldraft_round
+
+    w = weights16
+    P, bd, n_rounds, mid = 8192, 16, 40, 17
+    Kw = bd + 1
+    vis, ids = synthetic_prompt(cfg, 2048, P - 2048, seed=2)
+    emb = torch.cat([vis, w["embed"][ids]], 0)
+    n_ar = n_rounds * (Kw + 1) + 1
+    eng = GssEngine(cfg, w, max_bs=1, max_len=P + n_ar + 2 * Kw + 64, device=cuda)
+    dec = SelfSpecDecoder(eng, bd=bd, mask_id=cfg.vocab - 1, bs=1, max_rounds=n_ar + 8)
+    print("prefill 8192", flush=True)
+    last = eng.prefill(0, emb)
+    x00 = last.float().argmax().view(1)
+
+    def reset():
+        eng.seq_lens[:1].fill_(P)
+        dec.start(x00)
+
+    reset()
+    dec.round()
+    reset()
+    dec.ar_step()
+    reset()
+    dec.capture()
+    # AR: graph-replayed one-row steps
+    reset()
+    for _ in range(n_ar):
+        dec.g_ar.replay()
+    torch.cuda.synchronize()
+    ar = [int(x00)] + dec.ar_log[:n_ar, 0].cpu().tolist()
+    print("AR done", flush=True)
+
+    # spec: graph-replayed rounds; round `mid` is inspected
+    reset()
+    for _ in range(mid):
+        dec.g_round.replay()
+    torch.cuda.synchronize()
+    S = int(eng.seq_lens[0])
+    x0 = int(dec.st.x0[0])
+    pt = eng.page_table[0].cpu().numpy()
+    pgs = eng.page_table[0, : (S + 15) // 16].long()
+    cache_kv = [(eng.k_pages[l][pgs].permute(0, 2, 1, 3).reshape(-1, cfg.n_kv_heads, cfg.head_dim)[:S].float().cpu(),
+                 eng.v_pages[l][pgs].permute(0, 3, 1, 2).reshape(-1, cfg.n_kv_heads, cfg.head_dim)[:S].float().cpu())
+                for l in range(cfg.n_layers)]
+    dec.g_round.replay()
+    torch.cuda.synchronize()
+    d_logits = dec.draft_b.logits.float().cpu()
+    v_bf16 = dec.verify_b.logits.cpu()
+    win = dec.st.am[0].cpu().numpy()
+    tgt = dec.st.tgt[0].cpu().numpy()
+    acc = int(dec.st.acc[0])
+    packed = dec.st.packed[0].cpu().numpy()
+    slots = dec.st.slots[0].cpu().numpy()
+    S_after = int(eng.seq_lens[0])
+    x0_next = int(dec.st.x0[0])
+    for _ in range(n_rounds - mid - 1):
+        dec.g_round.replay()
+    torch.cuda.synchronize()
+
+    # (1) committed ids == AR ids, bit for bit
+    spec = [int(x00)] + dec.committed(n_rounds)[0]
+    accs = dec.accept_lengths(n_rounds)[:, 0]
+    print(f"{len(spec)} ids in {n_rounds} rounds; accept histogram {np.bincount(accs, minlength=Kw).tolist()}",
+          flush=True)
+    assert len(spec) >= 2 * n_rounds + 1
+    assert spec == ar[:len(spec)]
+
+    # (2) integer outputs of round `mid`, bit-exact against the oracle's rules on the GPU's own logits
+    t_ref = argmax_first(v_bf16.float().numpy().reshape(Kw, -1))
+    assert (tgt == t_ref).all()
+    acc_ref = int(accept_chain(win[None], t_ref[None])[0])
+    assert acc == acc_ref
+    want = np.zeros(Kw + 2, dtype=np.int64)
+    want[0], want[1] = win[0], acc_ref
+    want[2:3 + acc_ref] = t_ref[: acc_ref + 1]
+    assert (packed == want).all(), (packed, want)
+    assert x0_next == int(t_ref[acc_ref]) and S_after == S + acc_ref + 2
+    slots_ref = [page_slot(pt, S + 1 + j) if j <= acc_ref else -1 for j in range(Kw)]
+    assert slots.tolist() == slots_ref
+
+    # (3) the same round through the fp32 oracle from the same state
+    ocfg = DecoderConfig(n_layers=cfg.n_layers, hidden=cfg.hidden, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
+                         head_dim=cfg.head_dim, ffn=cfg.ffn, vocab=cfg.vocab)
+    om = OracleDecoder(ocfg, {k: v.bfloat16().float() for k, v in w.items()})
+    cache = KVCache(cfg.n_layers)
+    for l, (kk, vv) in enumerate(cache_kv):
+        cache.append(l, kk, vv)
+    trace = []
+    with torch.no_grad():
+        _, _, _, _, rec = fulldraft_round(om, cache, S, x0, bd, cfg.vocab - 1, trace=trace,
+                                          verify_window=win.tolist())
+    ed = float((d_logits[0] - trace[0]["draft_logits"]).abs().max())
+    ev = float((v_bf16[0].float() - trace[0]["verify_logits"]).abs().max())
+    print(f"round {mid}: S={S}, acc={acc}; logits vs fp32 oracle: draft {ed:.4f}, verify {ev:.4f}", flush=True)
+    assert ed <= LOGIT_ABS and ev <= LOGIT_ABS
+    vl = trace[0]["verify_logits"]
+    for r in range(Kw):
+        if int(rec["target"][r]) != int(tgt[r]):
+            top = torch.topk(vl[r].float(), 2).values
+            assert float(top[0] - top[1]) < TOL, (r, "verify argmax differs without a near tie")
+
+
+# ----------------------------------------------------------------------------------- 32 ragged sequences ----
+N_SEQ, ROUNDS = 32, 6
+
+
+@pytest.fixture(scope="module")
+def batched(cuda, weights16):
+    """A 32-sequence engine over one shuffled page pool with seeded random prefix K/V of ragged lengths, the batch's
+    AR decode (bs = 32, its attention plan) and, per sequence, the one-sequence AR decode under the same plan."""
+    from gravityocr_amd.engine import GssEngine, SelfSpecDecoder
+    from gravityocr_amd.model import SYNTH_1536 as cfg
+    rng = np.random.default_rng(3)
+    L0 = rng.integers(1024, 12289, size=N_SEQ).astype(np.int64)
+    n_ar = ROUNDS * (32 + 2) + 2
+    max_len = 12288 + n_ar + 2 * 34 + 64
+    eng = GssEngine(cfg, weights16, max_bs=N_SEQ, max_len=max_len, device=cuda, page_seed=3, max_win=34)
+    g = torch.Generator(device=cuda).manual_seed(3)
+    eng.k_pages.normal_(0.0, 0.8, generator=g)
+    eng.v_pages.normal_(0.0, 0.8, generator=g)
+    x0 = torch.tensor(rng.integers(0, cfg.vocab - 1, size=N_SEQ), dtype=torch.int32, device=cuda)
+    L0_dev = torch.tensor(L0, dtype=torch.int32, device=cuda)
+    plan = eng.attn_plan(N_SEQ)
+    print(f"32 sequences, prefixes {L0.min()}..{L0.max()} (sum {L0.sum()}), plan {plan}", flush=True)
+
+    dec = SelfSpecDecoder(eng, bd=8, mask_id=cfg.vocab - 1, bs=N_SEQ, max_rounds=n_ar + 8)
+    eng.seq_lens[:N_SEQ].copy_(L0_dev)
+    dec.start(x0)
+    g_ar = _capture_ar(dec)
+    eng.seq_lens[:N_SEQ].copy_(L0_dev)
+    dec.start(x0)
+    for _ in range(n_ar):
+        g_ar.replay()
+    torch.cuda.synchronize()
+    ar = torch.cat([x0.view(1, -1), dec.ar_log[:n_ar]], 0).t().contiguous()   # [bs, 1 + n_ar]: x0, then AR tokens
+    print("batched AR done", flush=True)
+
+    # one-sequence AR decodes under the batch's plan: each sequence alone reproduces its rows of the batch
+    for b in range(N_SEQ):
+        d1 = SelfSpecDecoder(eng, bd=8, mask_id=cfg.vocab - 1, bs=1, slot0=b, attn_plan=plan, max_rounds=n_ar + 8)
+        eng.seq_lens[b:b + 1].copy_(L0_dev[b:b + 1])
+        d1.start(x0[b:b + 1])
+        g1 = _capture_ar(d1)
+        eng.seq_lens[b:b + 1].copy_(L0_dev[b:b + 1])
+        d1.start(x0[b:b + 1])
+        for _ in range(n_ar):
+            g1.replay()
+        torch.cuda.synchronize()
+        alone = d1.ar_log[:n_ar, 0]
+        assert torch.equal(alone, ar[b, 1:]), f"sequence {b}: one-sequence AR differs from its batched AR"
+        del g1, d1
+    print("one-sequence AR decodes equal the batched AR", flush=True)
+    return dict(eng=eng, L0=L0, L0_dev=L0_dev, x0=x0, ar=ar, plan=plan)
+
+
+@pytest.mark.parametrize("planted", [False, True], ids=["own_drafts", "planted_drafts"])
+@pytest.mark.parametrize("bd", [8, 16, 32])
+def test_batched_rounds_equal_ar(cuda, batched, bd, planted):
+    from gravityocr_amd.engine import SelfSpecDecoder
+    from oracle.integer import page_slot
+    eng, L0, L0_dev, x0, ar = (batched[k] for k in ("eng", "L0", "L0_dev", "x0", "ar"))
+    V = eng.cfg.vocab
+    Kw = bd + 1
+    print(f"batched rounds B={bd} planted={planted}", flush=True)
+    dec = SelfSpecDecoder(eng, bd=bd, mask_id=V - 1, bs=N_SEQ, max_rounds=ROUNDS + 4)
+    hook = None
+    if planted:
+        rng = np.random.default_rng(100 + bd)
+        m = torch.tensor(np.minimum(rng.geometric(0.1, size=(ROUNDS + 4, N_SEQ)) - 1, bd), dtype=torch.int64,
+                         device=cuda)
+        jj = torch.arange(1, Kw, device=cuda)
+        arl = ar.to(torch.int64)
+
+        def hook():
+            st = dec.st
+            base = dec.sl.long() - L0_dev.long()                 # after the x0 commit: a0's index in the AR list
+            idx = (base[:, None] + jj[None, :]).clamp(max=arl.shape[1] - 1)
+            good = arl.gather(1, idx)
+            mm = m[st.ctr.clamp(max=m.shape[0] - 1)].view(-1)       # this round's planted match count per sequence
+            st.am[:, 1:] = torch.where(jj[None, :] <= mm[:, None], good, (good + 1) % V).to(torch.int32)
+
+    eng.seq_lens[:N_SEQ].copy_(L0_dev)
+    dec.start(x0)
+    pt = eng.page_table[:N_SEQ].cpu().numpy()
+    for r in range(ROUNDS):
+        S = eng.seq_lens[:N_SEQ].cpu().numpy().astype(np.int64)
+        dec.round(after_draft=hook)
+        torch.cuda.synchronize()
+        acc = dec.st.acc.cpu().numpy()
+        slots = dec.st.slots.cpu().numpy()
+        assert (eng.seq_lens[:N_SEQ].cpu().numpy() == S + acc + 2).all(), r
+        for b in range(N_SEQ):
+            want = [page_slot(pt[b], int(S[b]) + 1 + j) if j <= acc[b] else -1 for j in range(Kw)]
+            assert slots[b].tolist() == want, (r, b)
+    accs = dec.accept_lengths(ROUNDS)
+    spec = dec.committed(ROUNDS)
+    for b in range(N_SEQ):
+        assert spec[b] == ar[b, 1:1 + len(spec[b])].tolist(), f"sequence {b} differs from its AR decode"
+    hist = np.bincount(accs.reshape(-1), minlength=Kw).tolist()
+    print(f"B={bd} planted={planted}: {sum(len(s) for s in spec)} ids, accept histogram {hist}", flush=True)
+    if planted:
+        assert len(set(accs.reshape(-1).tolist())) >= 3
