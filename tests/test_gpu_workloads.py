@@ -3,9 +3,13 @@ head_dim 128, SwiGLU 4608, vocab 59392, bf16, N(0, 0.02) weights, seed 2):
 
 bs = 1 rounds at an 8K prefix (2048 N(0,1) visual embeddings + 6144 ids, prefilled), B = 16, 40 graph-replayed rounds:
   * the committed ids equal the engine's own AR greedy decode (graph-replayed one-row steps) bit for bit;
-  * one mid-run round, replayed through the fp32 oracle from the same state (the GPU's KV cache, x0 and, for the
-    verify half, the GPU's verify window): draft and verify logits within the bf16 logit tolerance (2e-2), and the
-    oracle's verify argmax equal to the GPU's except where the oracle's own top-2 gap is below twice that;
+  * one mid-run round, replayed through the oracle from the same state (the GPU's KV cache, x0 and, for the verify
+    half, the GPU's verify window) in fp32 and in bf16 (the bf16 module's rounding points, the arithmetic the
+    reference's own bf16 model runs): the GPU's draft and verify logits are no further from the fp32 round than
+    the bf16 oracle is (max and mean |error| within 1.25x of the bf16 oracle's; on this 16-layer model both sit
+    near 0.05 max / 0.008 mean for logits of spread 0.78, so the 2e-2 max bound the smaller decoders meet is
+    not reachable by any bf16 evaluation here), and the fp32 oracle's verify argmax equals the GPU's except where
+    its own top-2 gap is below twice the bf16 logit tolerance;
   * that round's integer outputs bit-exact against the oracle's integer rules applied to the GPU's logits: targets
     (first-index argmax of the bf16 rows), accept length (linear chain), packed row, next x0, committed length and
     the paged-KV slot of every committed row (page_table[pos // 16] * 16 + pos % 16).
@@ -132,22 +136,32 @@ def test_bs1_rounds_at_8k_prefix(cuda, weights16):
     slots_ref = [page_slot(pt, S + 1 + j) if j <= acc_ref else -1 for j in range(Kw)]
     assert slots.tolist() == slots_ref
 
-    # (3) the same round through the fp32 oracle from the same state
+    # (3) the same round through the oracle from the same state, in fp32 and in the bf16 module's arithmetic
     ocfg = DecoderConfig(n_layers=cfg.n_layers, hidden=cfg.hidden, n_heads=cfg.n_heads, n_kv_heads=cfg.n_kv_heads,
                          head_dim=cfg.head_dim, ffn=cfg.ffn, vocab=cfg.vocab)
-    om = OracleDecoder(ocfg, {k: v.bfloat16().float() for k, v in w.items()})
-    cache = KVCache(cfg.n_layers)
-    for l, (kk, vv) in enumerate(cache_kv):
-        cache.append(l, kk, vv)
-    trace = []
-    with torch.no_grad():
-        _, _, _, _, rec = fulldraft_round(om, cache, S, x0, bd, cfg.vocab - 1, trace=trace,
-                                          verify_window=win.tolist())
-    ed = float((d_logits[0] - trace[0]["draft_logits"]).abs().max())
-    ev = float((v_bf16[0].float() - trace[0]["verify_logits"]).abs().max())
-    print(f"round {mid}: S={S}, acc={acc}; logits vs fp32 oracle: draft {ed:.4f}, verify {ev:.4f}", flush=True)
-    assert ed <= LOGIT_ABS and ev <= LOGIT_ABS
-    vl = trace[0]["verify_logits"]
+    wb = {k: v.bfloat16().float() for k, v in w.items()}
+    rounds = {}
+    for name, dt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        om = OracleDecoder(ocfg, wb, dtype=dt)
+        cache = KVCache(cfg.n_layers)
+        for l, (kk, vv) in enumerate(cache_kv):
+            cache.append(l, kk.to(dt), vv.to(dt))
+        trace = []
+        with torch.no_grad():
+            _, _, _, _, rec = fulldraft_round(om, cache, S, x0, bd, cfg.vocab - 1, trace=trace,
+                                              verify_window=win.tolist())
+        rounds[name] = (trace[0]["draft_logits"].float(), trace[0]["verify_logits"].float(), rec)
+    # the engine's logits buffers are [rows, V] (rows = bs * K; bs = 1 here)
+    f32_d, f32_v, rec = rounds["f32"]
+    assert d_logits.shape == f32_d.shape == v_bf16.shape
+    for name, gpu, ref, bf in (("draft", d_logits, f32_d, rounds["bf16"][0]),
+                               ("verify", v_bf16.float(), f32_v, rounds["bf16"][1])):
+        e_gpu, e_bf = (gpu - ref).abs(), (bf - ref).abs()
+        print(f"round {mid} {name}: |GPU - fp32| max {float(e_gpu.max()):.4f} mean {float(e_gpu.mean()):.5f}; "
+              f"|bf16 oracle - fp32| max {float(e_bf.max()):.4f} mean {float(e_bf.mean()):.5f}", flush=True)
+        assert float(e_gpu.max()) <= 1.25 * float(e_bf.max()), name
+        assert float(e_gpu.mean()) <= 1.25 * float(e_bf.mean()), name
+    vl = f32_v
     for r in range(Kw):
         if int(rec["target"][r]) != int(tgt[r]):
             top = torch.topk(vl[r].float(), 2).values
