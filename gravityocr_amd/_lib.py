@@ -25,7 +25,7 @@ SIGNATURES = {
     "gss_unmask_step": ([_p, _i, _i64, _i, _i, _i, _p, _i, _f, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
     "gss_kv_commit_workspace_size": ([_i, _psz], _i),
     "gss_kv_commit": ([_p, _p, _i64, _p, _p, _i64, _p, _i, _p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p], _i),
-    "gss_ss_commit": ([_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _p], _i),
+    "gss_ss_commit": ([_p, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _i64, _i, _i, _i, _p, _p, _p, _p], _i),
     "gss_kv_meta": ([_p, _i64, _i64, _p, _p, _i, _p, _p, _i64, _i, _p], _i),
     "gss_log_append": ([_p, _i, _p, _p, _i, _p, _p, _i, _p, _p, _i, _p], _i),
     "gss_penalize_rows": ([_p, _i64, _i, _i, _i, _p, _p, _p], _i),
@@ -59,6 +59,12 @@ class AttnPlan(ctypes.Structure):
 
     def __repr__(self):
         return "AttnPlan(kernel=%d, tiles_per_split=%d, n_split=%d, max_kv_len=%d)" % self.key()
+
+
+class FinishRule(ctypes.Structure):
+    """gss_finish_rule (include/gss.h): per-request budget, stop ids and vocabulary bound of the cut rule."""
+    _fields_ = [("budget", ctypes.c_void_p), ("stop_ids", ctypes.c_void_p), ("n_stop", ctypes.c_int),
+                ("vocab", ctypes.c_void_p)]
 
 
 class NormEpilogue(ctypes.Structure):

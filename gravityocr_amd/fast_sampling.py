@@ -20,6 +20,9 @@ layers, norm), ``glm.lm_head``, ``mm_model`` (get_image_features, get_rope_index
 ``mask_id``, ``image_token_id``, ``bd_size``. Image preprocessing and the prompt embedding (the vision tower) run
 through the model's own modules, as in the reference; everything from the prefill on runs on the kernels.
 
+``generate_speculative_prefixcache`` (src/fast_sampling.py:262-422) runs on the same rounds: its committed ids are
+those of its causal verify, i.e. AR greedy decoding, which these rounds reproduce (see its docstring).
+
 Supported arguments: greedy decoding (``temperature == 0``), ``draft_steps == 1``, ``accept_conf == 0`` and
 ``full_draft=True`` -- the reference's defaults. Other values raise NotImplementedError (no silent fallback).
 """
@@ -34,8 +37,8 @@ from .diffusion import BlockDiffusionDecoder
 from .engine import PAGE, GssEngine, SelfSpecDecoder
 from .model import config_from_model, weights_from_model
 
-__all__ = ["generate_speculative_natcache", "generate_cached", "teacher_force_argmax", "enable_fused_flex",
-           "prepare_prompt"]
+__all__ = ["generate_speculative_natcache", "generate_speculative_prefixcache", "generate_cached",
+           "teacher_force_argmax", "enable_fused_flex", "prepare_prompt"]
 
 _MIN_CAPACITY = 4096
 
@@ -167,6 +170,57 @@ def _decode_text(model, gen: List[int], device) -> str:
     return re.sub(r"<think>.*?</think>\s*", "", txt, flags=re.S)
 
 
+def _spec_rounds(model, image, prompt, max_new_tokens, max_long_side, bd):
+    """Prompt, prefill and the full-draft rounds of the cached self-spec decode on the engine. Returns (the packed
+    row of every round that counts, the decoder, the tokenizer's EOS id, the device)."""
+    device = _model_device(model)
+    mask_id = int(model.mask_id)
+    eos_id = model.tokenizer.eos_token_id
+    input_ids, emb, positions, next_pos = prepare_prompt(model, image, prompt, max_long_side, device)
+    P = input_ids.shape[1]
+    # capacity: prompt + budget + the last round's overshoot (bd + 2) + one look-ahead round + a window
+    sess = _session(model, device, P + max_new_tokens + 3 * (bd + 2) + PAGE)
+    eng = sess.eng
+    dec = sess.decoder(bd, mask_id)
+    if max_new_tokens <= 0:
+        return [], dec, eos_id, device
+    seed_logit = _prefill(eng, emb, positions)
+    a0 = _argmax_rows(eng, seed_logit.view(1, -1), softmax_rule=True)
+    dec.start(a0, pos_delta=torch.full((1,), next_pos - P, dtype=torch.int32, device=device))
+    return _run_rounds(sess, dec, (bd, mask_id), bd, max_new_tokens, eos_id), dec, eos_id, device
+
+
+def _finish(model, log_rows, dec, eos_id, device, bd, return_stats, trace, seed_key):
+    """Committed ids, the trace entries and the text / stats of the drop-ins (src/fast_sampling.py:608-628)."""
+    n_rounds = len(log_rows)
+    committed: List[int] = []
+    for row in log_rows:
+        committed.append(row[0])
+        committed.extend(row[2:3 + row[1]])
+    if trace is not None:
+        am = dec.log_am[:n_rounds, 0].cpu().tolist()
+        tg = dec.log_tgt[:n_rounds, 0].cpu().tolist()
+        for r, row in enumerate(log_rows):
+            acc = row[1]
+            k = bd + 1 if acc == bd else acc + 1
+            ar_pred = [am[r][0]] + tg[r][:bd]
+            entry = {"round": r + 1, "k": k}
+            if seed_key:
+                entry["seed"] = ar_pred[0]
+            entry.update({"draft": am[r], "ar_pred": ar_pred, "new_tokens": [row[0]] + row[2:3 + acc]})
+            trace.append(entry)
+    gen = committed
+    if eos_id is not None and eos_id in gen:
+        gen = gen[:gen.index(eos_id)]
+    txt = _decode_text(model, gen, device)
+    if return_stats:
+        fwd = 2 * n_rounds
+        return txt, {"rounds": n_rounds, "draft_fwd": n_rounds, "verify_fwd": n_rounds, "commit_fwd": 0,
+                     "total_fwd": fwd, "resp_tokens": len(gen), "tokens_per_fwd": round(len(gen) / max(1, fwd), 3),
+                     "accept_per_round": round(len(committed) / max(1, n_rounds), 2)}
+    return txt
+
+
 @torch.no_grad()
 def generate_speculative_natcache(model, image, prompt="Text Recognition:", max_new_tokens=512,
                                   draft_threshold=0.9, temperature=0.0, top_p=0.95,
@@ -179,49 +233,31 @@ def generate_speculative_natcache(model, image, prompt="Text Recognition:", max_
     the reference's iterative-unmask and sampling branches, which this path rejects (see the module docstring).
     """
     _check_greedy(temperature, accept_conf, draft_steps, full_draft)
-    device = _model_device(model)
     bd = int(draft_bd) if draft_bd else int(model.bd_size)
-    mask_id = int(model.mask_id)
-    eos_id = model.tokenizer.eos_token_id
-    input_ids, emb, positions, next_pos = prepare_prompt(model, image, prompt, max_long_side, device)
-    P = input_ids.shape[1]
-    # capacity: prompt + budget + the last round's overshoot (bd + 2) + one look-ahead round + a window
-    sess = _session(model, device, P + max_new_tokens + 3 * (bd + 2) + PAGE)
-    eng = sess.eng
-    dec = sess.decoder(bd, mask_id)
-    key = (bd, mask_id)
+    rows, dec, eos_id, device = _spec_rounds(model, image, prompt, max_new_tokens, max_long_side, bd)
+    return _finish(model, rows, dec, eos_id, device, bd, return_stats, trace, seed_key=False)
 
-    if max_new_tokens <= 0:
-        log_rows: List[List[int]] = []
-    else:
-        seed_logit = _prefill(eng, emb, positions)
-        a0 = _argmax_rows(eng, seed_logit.view(1, -1), softmax_rule=True)
-        dec.start(a0, pos_delta=torch.full((1,), next_pos - P, dtype=torch.int32, device=device))
-        log_rows = _run_rounds(sess, dec, key, bd, max_new_tokens, eos_id)
-    n_rounds = len(log_rows)
 
-    committed: List[int] = []
-    for row in log_rows:
-        committed.append(row[0])
-        committed.extend(row[2:3 + row[1]])
-    if trace is not None:
-        am = dec.log_am[:n_rounds, 0].cpu().tolist()
-        tg = dec.log_tgt[:n_rounds, 0].cpu().tolist()
-        for r, row in enumerate(log_rows):
-            acc = row[1]
-            k = bd + 1 if acc == bd else acc + 1
-            trace.append({"round": r + 1, "k": k, "draft": am[r], "ar_pred": [am[r][0]] + tg[r][:bd],
-                          "new_tokens": [row[0]] + row[2:3 + acc]})
-    gen = committed
-    if eos_id is not None and eos_id in gen:
-        gen = gen[:gen.index(eos_id)]
-    txt = _decode_text(model, gen, device)
-    if return_stats:
-        fwd = 2 * n_rounds
-        return txt, {"rounds": n_rounds, "draft_fwd": n_rounds, "verify_fwd": n_rounds, "commit_fwd": 0,
-                     "total_fwd": fwd, "resp_tokens": len(gen), "tokens_per_fwd": round(len(gen) / max(1, fwd), 3),
-                     "accept_per_round": round(len(committed) / max(1, n_rounds), 2)}
-    return txt
+@torch.no_grad()
+def generate_speculative_prefixcache(model, image, prompt="Text Recognition:", max_new_tokens=512,
+                                     draft_threshold=0.9, temperature=0.0, top_p=0.95,
+                                     max_long_side=1344, accept_conf=0.0, draft_steps=1,
+                                     return_stats=False, trace=None, full_draft=True):
+    """The prefix-cached self-speculative decode (src/fast_sampling.py:262-422) on the MI355X kernels: same
+    arguments, return value and stats keys; ``trace`` entries {"round", "k", "seed", "draft", "ar_pred",
+    "new_tokens"}.
+
+    The reference caches only the prompt and re-forwards the committed response every round, the draft under a
+    bd-grid block-causal mask and the verify causally (:325-338). Its committed ids are those of the causal
+    verify, i.e. AR greedy decoding (:391-416); the draft's mask decides only how many of them a round accepts.
+    Here the rounds are the engine's cached full-draft rounds (the committed response's K/V kept, not re-forwarded;
+    the draft [pending | MASK x bd] against it), so the committed ids are the same AR greedy ids while the
+    per-round acceptance, and with it ``rounds`` / ``accept_per_round`` and the trace's draft entries, follow the
+    cached draft. Greedy, one draft step, full draft only, as the natcache drop-in."""
+    _check_greedy(temperature, accept_conf, draft_steps, full_draft)
+    bd = int(model.bd_size)
+    rows, dec, eos_id, device = _spec_rounds(model, image, prompt, max_new_tokens, max_long_side, bd)
+    return _finish(model, rows, dec, eos_id, device, bd, return_stats, trace, seed_key=True)
 
 
 def _run_rounds(sess: _Session, dec: SelfSpecDecoder, key, bd: int, max_new_tokens: int, eos_id) -> List[List[int]]:

@@ -5,7 +5,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import AttnPlan, NormEpilogue, NormPrologue, Penalties, check, lib
+from ._lib import AttnPlan, FinishRule, NormEpilogue, NormPrologue, Penalties, check, lib
 
 PAGE = 16
 ATTN_ROWGROUP, ATTN_WIDE = 0, 1
@@ -192,10 +192,13 @@ def kv_commit(k_win, v_win, k_pages, v_pages, page_table, seq_lens, workspace, *
                               _stream()), "gss_kv_commit")
 
 
-def ss_commit(predict, accept_len, a0, req_pool_indices, seeds, seq_lens, loc, packed, free_slots, out, *, K: int):
+def ss_commit(predict, accept_len, a0, req_pool_indices, seeds, seq_lens, loc, packed, free_slots, out, *, K: int,
+              page: int = 1, budget=None, stop_ids=None, vocab=None, cut=None, n_free=None):
     """The serving round's commit bookkeeping (gss_ss_commit). predict int32 [>= bs*K]; accept_len int32 [bs];
     a0 int64 [bs] (any stride); req_pool_indices int64 [bs]; seeds int64 [pool]; seq_lens int64 [bs] (in place);
-    loc int64 [bs*K]; packed int32 [bs, K+2]; free_slots int64 [bs*K]; out int64 [bs]."""
+    loc int64 [bs*K]; packed int32 [bs, K+2]; free_slots int64 [bs*K]; out int64 [bs]. ``page``: the KV page size
+    of the slots. The finish rule (optional, all three): budget / vocab int32 [bs], stop_ids int32 [bs, n_stop];
+    cut int32 [bs] and n_free int32 [1] receive the cut index and the free-list length."""
     bs = accept_len.shape[0]
     _need(accept_len, torch.int32, "accept_len", (bs,))
     if predict.dtype != torch.int32 or not predict.is_contiguous() or predict.numel() < bs * K:
@@ -209,9 +212,23 @@ def ss_commit(predict, accept_len, a0, req_pool_indices, seeds, seq_lens, loc, p
     _need(packed, torch.int32, "packed", (bs, K + 2))
     _need(free_slots, torch.int64, "free_slots", (bs * K,))
     _need(out, torch.int64, "out", (bs,))
+    rule = None
+    if budget is not None or stop_ids is not None or vocab is not None:
+        if budget is None or vocab is None or stop_ids is None:
+            raise ValueError("the finish rule needs budget, stop_ids and vocab")
+        _need(budget, torch.int32, "budget", (bs,))
+        _need(vocab, torch.int32, "vocab", (bs,))
+        _need(stop_ids, torch.int32, "stop_ids", (bs, stop_ids.shape[1]))
+        rule = FinishRule(budget.data_ptr(), stop_ids.data_ptr() if stop_ids.numel() else 0, stop_ids.shape[1],
+                          vocab.data_ptr())
+    if cut is not None:
+        _need(cut, torch.int32, "cut", (bs,))
+    if n_free is not None:
+        _need(n_free, torch.int32, "n_free", (1,))
     check(lib().gss_ss_commit(_ptr(predict), _ptr(accept_len), _ptr(a0), a0.stride(0), _ptr(req_pool_indices),
                               _ptr(seeds), _ptr(seq_lens), _ptr(loc), _ptr(packed), _ptr(free_slots), _ptr(out),
-                              seeds.numel(), bs, K, _stream()), "gss_ss_commit")
+                              seeds.numel(), bs, K, int(page), None if rule is None else ctypes.byref(rule),
+                              _ptr(cut), _ptr(n_free), _stream()), "gss_ss_commit")
 
 
 def kv_meta(req_to_token, req_pool_indices, seq_lens, kv_indptr, kv_indices, *, extra: int):

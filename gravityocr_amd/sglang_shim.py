@@ -12,15 +12,15 @@ and the KV pool keeps the kernels' layout (``PagedKVPool``; SGLang's set_kv_buff
 Roles: a draft forward [x0 | MASK x (K-1)] runs gss_draft_attn with its first row causal (the reference's
 NON_CAUSAL mask rows + CAUSAL seed row), a verify forward gss_verify_attn (causal, bottom-right aligned); the prefix
 is the request's committed length (forward_batch.seq_lens) read from the pages, the window's own K/V from the
-forward's k / v. The commit runs gss_ss_commit (packed row, seeds, seq_lens, compacted free list) and the reference's
-host bookkeeping over one page-locked readback.
+forward's k / v. The commit (GssFastCommit) runs gss_ss_commit: packed rows, seeds, the finish cut of every
+request, seq_lens and the page-granular free list in one launch, then one page-locked readback and one extend +
+check_finished per request.
 """
-from typing import Optional
+from typing import Callable, List, Optional
 
 import torch
 
 from . import kernels as gk
-from .selfspec_commit_rules import host_commit
 
 PAGE = 16
 ROLE_DRAFT, ROLE_VERIFY = "draft", "verify"
@@ -75,6 +75,12 @@ class GssSelfSpecAttnBackend:
         rpi = forward_batch.req_pool_indices.to(torch.int64)
         if self.req_to_token.shape[1] < self.max_pages * PAGE:
             raise ValueError("req_to_token rows are shorter than max_kv_len")
+        # the kernels read at most max_kv_len prefix keys (the plan's capacity): a longer request would lose its
+        # last keys, so it is an error here, where the host copy of the lengths is at hand
+        sl_cpu = getattr(forward_batch, "seq_lens_cpu", None)
+        if sl_cpu is not None and len(sl_cpu) and int(sl_cpu.max()) > self.max_kv_len:
+            raise ValueError(f"a request's kv length {int(sl_cpu.max())} exceeds the backend's max_kv_len "
+                             f"{self.max_kv_len}")
         self.page_table = (self.req_to_token[rpi, : self.max_pages * PAGE : PAGE] // PAGE).to(torch.int32).contiguous()
         self.prefix = forward_batch.seq_lens.to(torch.int32).contiguous()
 
@@ -97,54 +103,150 @@ class GssSelfSpecAttnBackend:
         return o.view(bs * W, self.Hq * self.D)
 
 
-class GssFastCommit:
-    """SelfSpecFastCommit.commit on gss_ss_commit: the round's device bookkeeping in one launch, one page-locked
-    readback, then the reference's host bookkeeping (host_commit, lengths, frees of the rejected verify slots)."""
+def _round_up(x: int, m: int) -> int:
+    return -(-x // m) * m
 
-    def __init__(self, K: int, max_bs: int, device):
-        self.K, self.max_bs, self.device = K, max_bs, device
-        self.packed_dev = torch.zeros(max_bs, K + 2, dtype=torch.int32, device=device)
-        self.packed_host = torch.zeros(max_bs, K + 2, dtype=torch.int32, pin_memory=True)
+
+def stop_ids_of(req) -> List[int]:
+    """The token ids that end a request (SGLang's token-based finish check: the request's stop_token_ids, its
+    eos_token_ids and the tokenizer's eos and additional stop ids), none with ignore_eos."""
+    sp = req.sampling_params
+    if sp.ignore_eos:
+        return []
+    tk = req.tokenizer
+    ids = list(sp.stop_token_ids or ()) + list(req.eos_token_ids or ())
+    if tk is not None:
+        ids += [tk.eos_token_id] if tk.eos_token_id is not None else []
+        ids += list(getattr(tk, "additional_stop_token_ids", None) or ())
+    return sorted(set(int(x) for x in ids))
+
+
+def cut_rule_applies(req) -> bool:
+    """Whether the device cut rule decides this request's finish: only length, stop ids and the vocabulary bound
+    can end it (no grammar to advance, no stop strings or regexes, no pending finish, not finished already)."""
+    sp = req.sampling_params
+    return (req.grammar is None and not req.to_finish and not req.finished() and not sp.stop_strs
+            and not sp.stop_regex_strs and req.vocab_size is not None)
+
+
+class GssFastCommit:
+    """The serving round's commit on gss_ss_commit at KV page size ``page``: one launch does the packed readback
+    rows, the seed pool, the cut index of every request (where its finish is decided by length, stop ids and the
+    vocabulary bound), seq_lens += cut and the free list of the verify slots in pages that hold no kept token; one
+    page-locked readback; then per request one extend of output_ids and one check_finished.
+
+    Requests the cut rule does not cover (grammar, stop strings / regexes, a pending finish) go through
+    ``token_loop(req, T) -> j``, the per-token append-and-check path (a deployment passes the reference's own,
+    selfspec_commit_rules.commit_slow, adapted to return j); without one such a request raises. When it stops
+    before the end of T, its device length and free pages are corrected on the stream (no extra sync)."""
+
+    def __init__(self, K: int, max_bs: int, device, page: int = PAGE, max_stop: int = 16,
+                 token_loop: Optional[Callable] = None):
+        self.K, self.max_bs, self.device, self.page = K, max_bs, device, page
+        self.max_stop = max_stop
+        self.token_loop = token_loop
+        i32 = dict(dtype=torch.int32)
+        self.packed_dev = torch.zeros(max_bs, K + 2, device=device, **i32)
+        self.cut_dev = torch.zeros(max_bs + 1, device=device, **i32)       # [bs] cut, then the free count
         self.free_dev = torch.zeros(max_bs * K, dtype=torch.int64, device=device)
+        # finish-rule inputs (budget, vocabulary bound, stop ids), staged in page-locked memory and copied on the
+        # stream before the launch
+        self.budget_host = torch.zeros(max_bs, pin_memory=True, **i32)
+        self.vocab_host = torch.zeros(max_bs, pin_memory=True, **i32)
+        self.stop_host = torch.zeros(max_bs, max_stop, pin_memory=True, **i32)
+        self.budget_dev = torch.zeros(max_bs, device=device, **i32)
+        self.vocab_dev = torch.zeros(max_bs, device=device, **i32)
+        self.stop_dev = torch.zeros(max_bs, max_stop, device=device, **i32)
+        self.packed_host = torch.zeros(max_bs, K + 2, pin_memory=True, **i32)
+        self.cut_host = torch.zeros(max_bs + 1, pin_memory=True, **i32)
         self.event = torch.cuda.Event()
         self.n_rounds = 0
+
+    def _stage_rules(self, reqs) -> None:
+        """Host values of the finish rule for this round's requests, then their copies to the device (queued on
+        the stream ahead of the commit kernel)."""
+        bs = len(reqs)
+        budget, vocab, stop = (t[:bs].numpy() for t in (self.budget_host, self.vocab_host, self.stop_host))
+        budget.fill(-1)                                   # -1: the per-token path decides
+        vocab.fill(0)
+        stop.fill(-1)
+        for i, req in enumerate(reqs):
+            if not cut_rule_applies(req):
+                continue
+            ids = stop_ids_of(req)
+            if len(ids) > self.max_stop:
+                raise ValueError(f"request has {len(ids)} stop ids, more than the {self.max_stop} staged")
+            budget[i] = max(0, req.sampling_params.max_new_tokens - len(req.output_ids))
+            vocab[i] = req.vocab_size
+            stop[i, :len(ids)] = ids
+        for h, d in ((self.budget_host, self.budget_dev), (self.vocab_host, self.vocab_dev),
+                     (self.stop_host, self.stop_dev)):
+            d[:bs].copy_(h[:bs], non_blocking=True)
 
     def commit(self, vi, batch, seeds: torch.Tensor, ahead=None):
         """Returns (next seeds device [bs], tokens per request, j per request)."""
         if ahead is not None:
             raise NotImplementedError("the draft-ahead commit is not built")
-        bs, Kw = batch.batch_size(), self.K
-        if vi.draft_token_num != Kw or bs > self.max_bs:
-            raise ValueError(f"commit: window {vi.draft_token_num} / batch {bs} vs {Kw} / {self.max_bs}")
+        reqs = batch.reqs
+        bs, K, pg = batch.batch_size(), self.K, self.page
+        if vi.draft_token_num != K or bs > self.max_bs:
+            raise ValueError(f"commit: window {vi.draft_token_num} / batch {bs} vs {K} / {self.max_bs}")
         loc = batch.out_cache_loc
+        S = batch.seq_lens_cpu.numpy().copy()             # verify row r of request i sits at position S[i] + r
+        self._stage_rules(reqs)
         out = torch.empty(bs, dtype=torch.int64, device=self.device)
         gk.ss_commit(vi.predict, vi.accept_length, vi.a0, batch.req_pool_indices, seeds, batch.seq_lens, loc,
-                    self.packed_dev[:bs], self.free_dev[: bs * Kw], out, K=Kw)
-        host = self.packed_host[:bs]
-        host.copy_(self.packed_dev[:bs], non_blocking=True)
+                     self.packed_dev[:bs], self.free_dev[: bs * K], out, K=K, page=pg, budget=self.budget_dev[:bs],
+                     vocab=self.vocab_dev[:bs], stop_ids=self.stop_dev[:bs], cut=self.cut_dev[:bs],
+                     n_free=self.cut_dev[bs:bs + 1])
+        self.packed_host[:bs].copy_(self.packed_dev[:bs], non_blocking=True)
+        self.cut_host[:bs + 1].copy_(self.cut_dev[:bs + 1], non_blocking=True)
         self.event.record()
-        self.event.synchronize()            # the round's one readback
-        rows = host.numpy().tolist()
-        toks, js, accs = host_commit(batch.reqs, rows)
-        sl = batch.seq_lens_cpu.numpy()
-        fix, n_free = False, 0
-        for i, req in enumerate(batch.reqs):
-            j, a = js[i], accs[i]
-            sl[i] += j
-            req.kv_committed_len += j + 1
-            req.kv_allocated_len = req.kv_committed_len
-            n_free += Kw - 1 - a
-            if j < a + 1:               # finished inside the round: the kernel advanced seq_lens by acc + 1
-                batch.seq_lens[i:i + 1].sub_(a + 1 - j)
-                fix = True
-        batch.seq_lens_sum += sum(js)
+        self.event.synchronize()                          # the round's one readback
+        rows = self.packed_host[:bs].numpy()
+        cuts = self.cut_host[:bs].numpy().tolist()
+        n_free = int(self.cut_host[bs])
         alloc = batch.token_to_kv_pool_allocator
-        if bs == 1:
-            alloc.free(loc[js[0]:])
-        elif fix:
-            alloc.free(torch.cat([loc[i * Kw + js[i]:(i + 1) * Kw] for i in range(bs)]))
-        elif n_free:
-            fl = self.free_dev[:n_free]
+        by_rule = self.budget_host[:bs].numpy() >= 0
+        extra_free = []
+        toks, js = [], []
+        for i, req in enumerate(reqs):
+            a = int(rows[i, 1])
+            T = [int(rows[i, 0])] + rows[i, 2:3 + a].tolist()
+            j = cuts[i]
+            if by_rule[i]:
+                req.output_ids.extend(T[: j + 1])
+                req.check_finished(j + 1)
+            else:
+                if self.token_loop is None:
+                    raise NotImplementedError("a request outside the cut rule (grammar, stop strings) needs the "
+                                              "per-token path: pass token_loop")
+                jl = int(self.token_loop(req, T))
+                if jl < j:
+                    # stopped inside the round: the device advanced seq_lens by j = a + 1 and freed the pages past
+                    # S + j; the kept rows end at S + jl, so the pages between the two page boundaries go as well
+                    batch.seq_lens[i:i + 1].sub_(j - jl)
+                    lo = _round_up(int(S[i]) + jl, pg) - int(S[i])
+                    hi = min(K, _round_up(int(S[i]) + j, pg) - int(S[i]))
+                    if hi > lo:
+                        extra_free.append(loc[i * K + lo:i * K + hi])
+                    j = jl
+            # acceptance counters: the verified count, or 0 when a0 itself ended the request
+            verified = 0 if (j == 0 and req.finished()) else a + 1
+            req.spec_verify_ct += 1
+            req.spec_accepted_tokens += verified
+            req.update_spec_acceptance_histogram(verified)
+            req.kv_committed_len += j + 1
+            req.kv_allocated_len = _round_up(req.kv_committed_len, pg)
+            toks.append(T[: j + 1])
+            js.append(j)
+        batch.seq_lens_cpu += torch.as_tensor(js, dtype=batch.seq_lens_cpu.dtype)
+        batch.seq_lens_sum += sum(js)
+        freed = [self.free_dev[:n_free]] if n_free else []
+        freed += extra_free
+        if freed:
+            fl = torch.cat(freed) if len(freed) > 1 else freed[0]
+            # inside a free group the allocator keeps the tensor itself: never hand it a view of a reused buffer
             alloc.free(fl if getattr(alloc, "is_not_in_free_group", True) else fl.clone())
         self.n_rounds += 1
         return out, toks, js

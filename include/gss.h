@@ -302,19 +302,34 @@ int gss_gemm_rope_stage(const void* x, int64_t ldx, const gss_norm_prologue* pro
  * request / slot layout. One wavefront per sequence; no workspace.
  *
  * gss_ss_commit replaces _ss_commit_kernel (patches/sglang/python/sglang/srt/speculative/selfspec_fast_commit.py:
- * 108-147): for row i with a = accept_len[i] (clamped into [0, K-1]):
+ * 108-147) and the cut rule of the host commit (selfspec_commit_rules.py:94-103, applied per request on the host
+ * there). For row i with a = accept_len[i] (clamped into [0, K-1]) and T = [a0, t_0 .. t_a]:
  *   packed[i]        = (int32(a0[i * a0_stride]), a, predict[i*K .. i*K+K-1] with entries past a zeroed)
  *   out[i]           = predict[i*K + a];  seeds[req_pool_indices[i]] = out[i]  (rows whose pool index is outside
  *                      [0, n_seeds) leave the pool untouched)
- *   seq_lens[i]     += a + 1
- *   free_slots       = loc[i*K + a+1 .. i*K + K-1] of every row, compacted in row order (sum(K-1-a) entries; the
- *                      buffer holds bs*K).
- * K <= 64.
+ *   j                = the cut index: T[:j + 1] is committed. Without a finish rule (finish == NULL) or for a row
+ *                      with budget[i] < 0 (a request whose finish needs the per-token path: grammar, stop strings),
+ *                      j = a + 1. Otherwise j = the first t < lim with T[t] in stop_ids[i, :] or T[t] > vocab[i] or
+ *                      T[t] < 0, else lim = min(a + 1, max(budget[i] - 1, 0)): where appending T one token at a time
+ *                      with SGLang's length / stop-token / vocabulary checks would stop.
+ *   cut[i] = j (cut may be NULL);  seq_lens[i] += j  (the verify rows 0 .. j-1 keep their KV)
+ *   free_slots       = the slots of rows j .. K-1 that lie in pages holding no kept token (page: the KV page size;
+ *                      slots are page-aligned, slot % page == position % page), every row's in row order, compacted;
+ *                      *n_free = their count (n_free may be NULL). With page = 1 and no finish rule this is the
+ *                      reference kernel's list: loc[i*K + a+1 .. i*K + K-1] of every row (sum(K-1-a) entries).
+ * One wavefront per sequence; K <= 64; stop_ids [bs, n_stop] (negative entries are padding).
  */
+typedef struct gss_finish_rule {
+  const int32_t* budget;   /* [bs] max_new_tokens - len(output_ids); < 0: the per-token path decides (j = a + 1) */
+  const int32_t* stop_ids; /* [bs, n_stop] */
+  int n_stop;
+  const int32_t* vocab;    /* [bs] the vocabulary bound of each request */
+} gss_finish_rule;
+
 int gss_ss_commit(const int32_t* predict, const int32_t* accept_len, const int64_t* a0, int64_t a0_stride,
                   const int64_t* req_pool_indices, int64_t* seeds, int64_t* seq_lens, const int64_t* loc,
-                  int32_t* packed, int64_t* free_slots, int64_t* out, int64_t n_seeds, int bs, int K,
-                  gss_stream_t stream);
+                  int32_t* packed, int64_t* free_slots, int64_t* out, int64_t n_seeds, int bs, int K, int page,
+                  const gss_finish_rule* finish, int32_t* cut, int32_t* n_free, gss_stream_t stream);
 
 /* gss_kv_meta replaces _ss_kv_meta_kernel (patches/sglang/python/sglang/srt/speculative/selfspec_fast_attn.py:
  * 104-132): the flattened KV index list of a batch for page size 1.

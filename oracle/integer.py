@@ -105,21 +105,26 @@ def committed_tokens(a0: int, target_row: Sequence[int], acc: int) -> List[int]:
 
 
 def ss_commit(predict: np.ndarray, acc: np.ndarray, a0: np.ndarray, rpi: np.ndarray, seeds: np.ndarray,
-              seq_lens: np.ndarray, loc: np.ndarray, K: int):
-    """Restatement of ``_ss_commit_kernel`` (patches/sglang/.../selfspec_fast_commit.py:108-147).
+              seq_lens: np.ndarray, loc: np.ndarray, K: int, page: int = 1, finish=None):
+    """Restatement of ``_ss_commit_kernel`` (patches/sglang/.../selfspec_fast_commit.py:108-147), with the host
+    commit's cut (selfspec_commit_rules.py:94-103 via ``cut_index_loop``) and page-granular frees.
 
-    Per request i with a = acc[i]:
+    Per request i with a = acc[i] and T = [a0, predict[i*K .. i*K + a]]:
       packed[i] = (a0[i], a, predict[i*K : i*K+K] with entries past a zeroed)
       seeds[rpi[i]] = out[i] = predict[i*K + a]
-      seq_lens[i] += a + 1
-      free list: slots loc[i*K + a+1 .. i*K + K-1], rows in order, compacted after the earlier rows' rejected slots.
-    Returns (packed [bs, K+2] int32, seeds', seq_lens', free [sum(K-1-acc)] int64, out [bs] int64).
-    """
+      j = a + 1 without ``finish`` or for budget < 0, else cut_index_loop(T, budget, stop, vocab)
+      seq_lens[i] += j
+      free list: slots loc[i*K + r], r = j .. K-1, whose position seq_lens[i] + r lies at or past the first page
+      boundary at or after seq_lens[i] + j (pages holding a kept token stay); rows in order. With page 1 and no
+      finish rule: loc[i*K + a+1 .. i*K + K-1], the reference kernel's list.
+    ``finish`` = (budgets, stops, vocabs) per request. Returns (packed [bs, K+2] int32, seeds', seq_lens',
+    free int64, out [bs] int64, cut [bs])."""
     bs = acc.shape[0]
     packed = np.zeros((bs, K + 2), dtype=np.int32)
     seeds = seeds.copy()
     seq_lens = seq_lens.copy()
     out = np.zeros(bs, dtype=np.int64)
+    cut = np.zeros(bs, dtype=np.int64)
     free = []
     for i in range(bs):
         a = int(acc[i])
@@ -130,9 +135,17 @@ def ss_commit(predict: np.ndarray, acc: np.ndarray, a0: np.ndarray, rpi: np.ndar
         s = int(predict[i * K + a])
         seeds[int(rpi[i])] = s
         out[i] = s
-        seq_lens[i] += a + 1
-        free.extend(int(loc[i * K + j]) for j in range(a + 1, K))
-    return packed, seeds, seq_lens, np.asarray(free, dtype=np.int64), out
+        T = [int(packed[i, 0])] + row[: a + 1]
+        if finish is None or finish[0][i] < 0:
+            j = a + 1
+        else:
+            j = cut_index_loop(T, int(finish[0][i]), finish[1][i], int(finish[2][i]))
+        cut[i] = j
+        S = int(seq_lens[i])
+        first_free = -(-(S + j) // page) * page
+        free.extend(int(loc[i * K + r]) for r in range(j, K) if S + r >= first_free)
+        seq_lens[i] += j
+    return packed, seeds, seq_lens, np.asarray(free, dtype=np.int64), out, cut
 
 
 def kv_meta(req_to_token: np.ndarray, rpi: np.ndarray, seq_lens: np.ndarray, extra: int):

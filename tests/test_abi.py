@@ -93,6 +93,12 @@ REFERENCE_SIGNATURES = {
         ("max_new_tokens", 512), ("draft_threshold", 0.9), ("temperature", 0.0), ("top_p", 0.95),
         ("max_long_side", 1344), ("accept_conf", 0.0), ("draft_steps", 1), ("return_stats", False),
         ("trace", None), ("draft_bd", None), ("full_draft", True)],
+    # src/fast_sampling.py:262-266
+    "generate_speculative_prefixcache": [
+        ("model", inspect.Parameter.empty), ("image", inspect.Parameter.empty), ("prompt", "Text Recognition:"),
+        ("max_new_tokens", 512), ("draft_threshold", 0.9), ("temperature", 0.0), ("top_p", 0.95),
+        ("max_long_side", 1344), ("accept_conf", 0.0), ("draft_steps", 1), ("return_stats", False),
+        ("trace", None), ("full_draft", True)],
     # src/fast_sampling.py:631-632
     "teacher_force_argmax": [("model", inspect.Parameter.empty), ("image", inspect.Parameter.empty),
                              ("prompt", inspect.Parameter.empty), ("gen_ids", inspect.Parameter.empty),
@@ -131,6 +137,12 @@ def test_dropin_rejects_unimplemented_modes_and_cpu_models():
             generate_speculative_natcache(m, None, **kw)
     with pytest.raises(RuntimeError, match="ROCm GPU"):
         generate_speculative_natcache(m, None)
+    from gravityocr_amd.fast_sampling import generate_speculative_prefixcache
+    for kw in (dict(temperature=0.7), dict(accept_conf=0.5), dict(draft_steps=2), dict(full_draft=False)):
+        with pytest.raises(NotImplementedError):
+            generate_speculative_prefixcache(m, None, **kw)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        generate_speculative_prefixcache(m, None)
     from gravityocr_amd.fast_sampling import generate_cached
     from gravityocr_amd.fast_sampling_batched import generate_cached_batched
     with pytest.raises(NotImplementedError):

@@ -33,7 +33,7 @@ def test_ss_commit_matches_oracle(cuda, bs, K):
     out = torch.full((bs,), -9, dtype=torch.int64, device=cuda)
     ss_commit(d(predict), d(acc), a0_dev, d(rpi), seeds_d, seq_d, d(loc), packed, free, out, K=K)
     torch.cuda.synchronize()
-    w_packed, w_seeds, w_seq, w_free, w_out = want
+    w_packed, w_seeds, w_seq, w_free, w_out, _ = want
     np.testing.assert_array_equal(packed.cpu().numpy(), w_packed)
     np.testing.assert_array_equal(seeds_d.cpu().numpy(), w_seeds)
     np.testing.assert_array_equal(seq_d.cpu().numpy(), w_seq)
@@ -41,6 +41,58 @@ def test_ss_commit_matches_oracle(cuda, bs, K):
     n = len(w_free)
     np.testing.assert_array_equal(free[:n].cpu().numpy(), w_free)
     assert bool((free[n:] == -9).all())                               # nothing written past the list
+
+
+@pytest.mark.parametrize("bs,K,page", [(1, 17, 16), (8, 5, 16), (33, 17, 16), (64, 33, 4), (130, 17, 16),
+                                       (7, 64, 16), (40, 9, 1)])
+def test_ss_commit_cut_rule_and_page_frees(cuda, bs, K, page):
+    """gss_ss_commit with the finish rule (per-request budgets, stop ids, vocabulary bounds; some requests marked for
+    the per-token path) and page-aligned slots: cut indices, lengths, packed rows, seeds and the page-granular free
+    list and its count bit-exact against the oracle (its cut is the per-token loop, its frees the page rule)."""
+    from gravityocr_amd.kernels import ss_commit
+    g = np.random.default_rng(bs * 7 + K + page)
+    V = 500
+    predict = g.integers(-3, V + 20, bs * K + 1).astype(np.int32)
+    acc = g.integers(0, K, bs).astype(np.int32)
+    a0 = g.integers(0, V, bs).astype(np.int64)
+    rpi = g.permutation(bs + 5)[:bs].astype(np.int64)
+    seeds = np.zeros(bs + 5, dtype=np.int64)
+    S = g.integers(0, 4000, bs).astype(np.int64)
+    n_pg = (4000 + K + page - 1) // page                                     # pages that cover a request
+    pts = [g.permutation(n_pg) + n_pg * i for i in range(bs)]
+    loc = np.array([pts[i][(S[i] + r) // page] * page + (S[i] + r) % page for i in range(bs) for r in range(K)],
+                   dtype=np.int64)
+    budgets = g.integers(-1, 2 * K, bs).astype(np.int32)
+    n_stop = 3
+    stop_ids = g.integers(-1, V, (bs, n_stop)).astype(np.int32)
+    stop_ids[:, 0] = -1                                                      # padding entries
+    # make some stop ids hit: a committed token of the row
+    for i in range(0, bs, 3):
+        stop_ids[i, 1] = predict[i * K + min(int(acc[i]), 1)]
+    vocab = g.integers(V - 5, V + 5, bs).astype(np.int32)
+    stops = [set(int(x) for x in row if x >= 0) for row in stop_ids]
+    w_packed, w_seeds, w_seq, w_free, w_out, w_cut = o_ss_commit(predict, acc, a0, rpi, seeds, S, loc, K, page=page,
+                                                                 finish=(budgets, stops, vocab))
+    d = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
+    seeds_d, seq_d = d(seeds), d(S)
+    packed = torch.full((bs, K + 2), -9, dtype=torch.int32, device=cuda)
+    free = torch.full((bs * K,), -9, dtype=torch.int64, device=cuda)
+    out = torch.full((bs,), -9, dtype=torch.int64, device=cuda)
+    cut = torch.full((bs,), -9, dtype=torch.int32, device=cuda)
+    n_free = torch.full((1,), -9, dtype=torch.int32, device=cuda)
+    ss_commit(d(predict), d(acc), d(a0), d(rpi), seeds_d, seq_d, d(loc), packed, free, out, K=K, page=page,
+              budget=d(budgets), stop_ids=d(stop_ids), vocab=d(vocab), cut=cut, n_free=n_free)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(cut.cpu().numpy(), w_cut)
+    np.testing.assert_array_equal(seq_d.cpu().numpy(), w_seq)
+    np.testing.assert_array_equal(packed.cpu().numpy(), w_packed)
+    np.testing.assert_array_equal(seeds_d.cpu().numpy(), w_seeds)
+    np.testing.assert_array_equal(out.cpu().numpy(), w_out)
+    n = len(w_free)
+    assert int(n_free[0]) == n
+    np.testing.assert_array_equal(free[:n].cpu().numpy(), w_free)
+    assert bool((free[n:] == -9).all())
+    print(f"bs={bs} K={K} page={page}: cuts {np.bincount(w_cut, minlength=K + 1).tolist()}, {n} slots freed")
 
 
 @pytest.mark.parametrize("bs,extra", [(1, 17), (5, 0), (32, 17), (200, 33)])

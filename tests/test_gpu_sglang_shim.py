@@ -2,8 +2,9 @@
   * set_kv_buffer writes each token's K/V to its slot in the kernels' page layout (read back exactly);
   * forward_extend for both roles equals the oracle's masked attention over the request's committed prefix (read
     through req_to_token's page-aligned slots) plus the window, within the attention tolerance (1e-2 * max |ref|);
-  * commit equals the oracle's _ss_commit restatement and host loop: next seeds, committed tokens and j, seq_lens
-    (device and host), and the freed rejected verify slots."""
+  * commit equals the oracle's _ss_commit restatement and per-token host loop: next seeds, committed tokens and j,
+    seq_lens (device and host), and, at page size 16, the freed pages: exactly the pages of the verify slots that hold
+    no kept token (a page-granular allocator would otherwise release committed KV)."""
 import numpy as np
 import pytest
 import torch
@@ -76,52 +77,98 @@ def test_attention_backend_matches_oracle(cuda, role):
         assert err <= 1e-2 * float(ref.abs().max()), (r, err)
 
 
-class _Alloc:
-    def __init__(self):
-        self.freed = []
+class _PageAlloc:
+    """SGLang's paged allocator as the commit sees it: free(slots) releases the pages those slots lie in."""
+
+    def __init__(self, page=16):
+        self.page, self.freed_pages, self.calls = page, [], 0
         self.is_not_in_free_group = True
 
     def free(self, t):
-        self.freed.append(t.clone())
+        self.calls += 1
+        self.freed_pages += sorted(set((t.cpu() // self.page).tolist()))
 
 
-@pytest.mark.parametrize("bs,finish", [(1, False), (4, False), (4, True)])
-def test_fast_commit_matches_oracle(cuda, bs, finish):
+def _token_loop(req, T):
+    """The per-token path for requests outside the cut rule: append one token, check, stop when finished."""
+    for t, x in enumerate(T):
+        req.output_ids.append(x)
+        req.check_finished()
+        if req.finished():
+            return t
+    return len(T) - 1
+
+
+@pytest.mark.parametrize("bs,finish", [(1, False), (4, False), (4, True), (16, True)])
+def test_fast_commit_pages_and_finish_rules(cuda, bs, finish):
+    """GssFastCommit at page size 16 on page-aligned verify slots: next seeds, committed tokens and cut j equal the
+    oracle's commit and per-token loop (stop ids 3 and 7, per-request budgets, vocabulary bound 10); every third
+    request (stop strings set) goes through the injected per-token path; seq_lens (device and host) advance by j;
+    the allocator is handed exactly the pages that hold no kept token (none holding a kept position), and the kv
+    lengths stay page-aligned."""
     from gravityocr_amd.sglang_shim import GssFastCommit
     print(f"shim commit bs={bs} finish={finish}", flush=True)
     g = np.random.default_rng(bs * 3 + finish)
-    K, vocab, pool_n = 5, 10, 8
+    K, vocab, pool_n, page = 17, 10, bs + 4, 16
     acc = g.integers(0, K, bs).astype(np.int32)
     predict = g.integers(0, 12, bs * K + 1).astype(np.int32)
     a0 = g.integers(0, 12, bs).astype(np.int64)
     rpi = g.permutation(pool_n)[:bs].astype(np.int64)
     seeds = g.integers(0, 100, pool_n).astype(np.int64)
-    sl = g.integers(10, 50, bs).astype(np.int64)
-    loc = g.permutation(200)[: bs * K].astype(np.int64)
-    budgets = [int(x) for x in g.integers(1, 3 if finish else 40, bs)]
+    S = g.integers(10, 200, bs).astype(np.int64)
+    pts = [g.permutation(64) + 64 * i for i in range(bs)]            # each request's own shuffled pages
+    loc = np.array([pts[i][(S[i] + r) // page] * page + (S[i] + r) % page for i in range(bs) for r in range(K)],
+                   dtype=np.int64)
+    budgets = [int(x) for x in g.integers(1, 3 if finish else 60, bs)]
     reqs = [_Req(bdg, vocab) for bdg in budgets]
+    slow = [i % 3 == 2 for i in range(bs)]
+    for i, r in enumerate(reqs):
+        r.kv_committed_len, r.kv_allocated_len = int(S[i]), int(S[i])
+        if slow[i]:
+            r.sampling_params.stop_strs = ["</s>"]
     dev = lambda a: torch.as_tensor(a).to(cuda)
     vi = _NS(predict=dev(predict), accept_length=dev(acc), a0=dev(a0), draft_token_num=K)
-    seeds_d, sl_d = dev(seeds), dev(sl)
+    seeds_d, sl_d = dev(seeds), dev(S)
+    alloc = _PageAlloc(page)
     batch = _NS(batch_size=lambda: bs, out_cache_loc=dev(loc), req_pool_indices=dev(rpi), seq_lens=sl_d,
-                seq_lens_cpu=torch.as_tensor(sl.copy()), seq_lens_sum=int(sl.sum()), reqs=reqs,
-                token_to_kv_pool_allocator=_Alloc())
-    for r in reqs:
-        r.kv_committed_len = r.kv_allocated_len = 0
-    fc = GssFastCommit(K, 8, cuda)
+                seq_lens_cpu=torch.as_tensor(S.copy()), seq_lens_sum=int(S.sum()), reqs=reqs,
+                token_to_kv_pool_allocator=alloc)
+    fc = GssFastCommit(K, 32, cuda, page=page, token_loop=_token_loop)
     out, toks, js = fc.commit(vi, batch, seeds_d)
     torch.cuda.synchronize()
-    packed, seeds_w, sl_w, free_w, out_w = o_ss_commit(predict, acc, a0, rpi, seeds.copy(), sl.copy(), loc, K)
+    packed, seeds_w, _, _, out_w, _ = o_ss_commit(predict, acc, a0, rpi, seeds.copy(), S.copy(), loc, K)
     otoks, ojs, oaccs = host_commit_loop(packed.tolist(), budgets, [{3, 7}] * bs, vocab)
     assert out.cpu().numpy().tolist() == out_w.tolist()
     assert np.array_equal(seeds_d.cpu().numpy(), seeds_w)
     assert toks == otoks and js == ojs
-    want_sl = sl + np.array(js)                    # device lengths after the finished-row fix
+    for i, r in enumerate(reqs):
+        assert r.output_ids == otoks[i]
+        assert r.kv_committed_len == S[i] + js[i] + 1 and r.kv_allocated_len % page == 0
+        assert r.kv_allocated_len >= r.kv_committed_len
+    want_sl = S + np.array(js)
     assert np.array_equal(sl_d.cpu().numpy(), want_sl) and np.array_equal(batch.seq_lens_cpu.numpy(), want_sl)
-    freed = torch.cat(batch.token_to_kv_pool_allocator.freed).cpu().numpy().tolist() if \
-        batch.token_to_kv_pool_allocator.freed else []
-    want_free = [int(s) for i in range(bs) for s in loc[i * K + js[i]:(i + 1) * K]]
-    if bs == 1 or any(j < a + 1 for j, a in zip(js, acc)):
-        assert freed == want_free
-    else:
-        assert freed == free_w.tolist() == want_free
+    assert batch.seq_lens_sum == int(S.sum()) + sum(js)
+    # pages: exactly those of the verify slots that hold no kept position [0, S + j)
+    want_pages = []
+    for i in range(bs):
+        kept = {int(pts[i][p // page]) for p in range(int(S[i]) + js[i])}
+        want_pages += sorted({int(loc[i * K + r]) // page for r in range(K)} - kept)
+        assert not kept & set(alloc.freed_pages)
+    assert sorted(alloc.freed_pages) == sorted(want_pages)
+    assert alloc.calls <= 1
+
+
+def test_fast_commit_without_token_loop_raises_for_slow_requests(cuda):
+    from gravityocr_amd.sglang_shim import GssFastCommit
+    K = 5
+    req = _Req(10, 10)
+    req.sampling_params.stop_strs = ["</s>"]
+    req.kv_committed_len = req.kv_allocated_len = 16
+    dev = lambda a: torch.as_tensor(a).to(cuda)
+    vi = _NS(predict=dev(np.arange(K + 1, dtype=np.int32)), accept_length=dev(np.array([1], dtype=np.int32)),
+             a0=dev(np.array([4], dtype=np.int64)), draft_token_num=K)
+    batch = _NS(batch_size=lambda: 1, out_cache_loc=dev(np.arange(16, 16 + K, dtype=np.int64)),
+                req_pool_indices=dev(np.array([0])), seq_lens=dev(np.array([16])),
+                seq_lens_cpu=torch.tensor([16]), seq_lens_sum=16, reqs=[req], token_to_kv_pool_allocator=_PageAlloc())
+    with pytest.raises(NotImplementedError):
+        GssFastCommit(K, 4, cuda).commit(vi, batch, dev(np.zeros(2, dtype=np.int64)))

@@ -96,7 +96,8 @@ def test_ss_commit_reference_invariants(bs, K, seed):
     seeds = np.zeros(bs + 3, dtype=np.int64)
     seq = g.integers(0, 5000, bs)
     loc = g.integers(0, 10**6, bs * K)
-    packed, seeds2, seq2, free, out = ss_commit(predict, acc, a0, rpi, seeds, seq, loc, K)
+    packed, seeds2, seq2, free, out, cut = ss_commit(predict, acc, a0, rpi, seeds, seq, loc, K)
+    assert cut.tolist() == (acc + 1).tolist()
     want_free = [int(loc[i * K + t]) for i in range(bs) for t in range(int(acc[i]) + 1, K)]
     assert free.tolist() == want_free
     assert len(free) == int(sum(K - 1 - acc))
@@ -131,12 +132,37 @@ def test_page_slot_is_flattened_page_order():
         assert page_slot(pt, pos) == flat[pos]
 
 
-@settings(max_examples=500, deadline=None)
-@given(st.lists(st.integers(-2, 12), min_size=1, max_size=10), st.integers(-2, 12),
-       st.sets(st.integers(0, 12), max_size=3), st.integers(5, 11))
-def test_product_cut_index_equals_per_token_loop(T, budget, stop, vocab):
-    from gravityocr_amd.selfspec_commit_rules import cut_index
-    assert cut_index(T, budget, frozenset(stop), vocab) == cut_index_loop(T, budget, stop, vocab)
+@settings(max_examples=300, deadline=None)
+@given(st.integers(1, 6), st.integers(2, 20), st.sampled_from([1, 4, 16]), st.integers(0, 10**6))
+def test_ss_commit_paged_frees_by_page_sets(bs, K, page, seed):
+    """The free list of the paged commit, against its definition as page sets: each request's slots are page-aligned
+    (its own shuffled pages, position p at page_table[p // page] * page + p % page); after the cut j the kept
+    positions are [0, S + j); a verify slot is freed iff its page holds no kept position. The finish rule's cut is
+    checked against the per-token loop by the same function (rows with budget < 0 keep every token)."""
+    g = np.random.default_rng(seed)
+    n_pages = 64
+    predict = g.integers(-1, 12, bs * K + 1)
+    acc = g.integers(0, K, bs)
+    a0 = g.integers(0, 12, bs)
+    rpi = g.permutation(bs + 3)[:bs]
+    seeds = np.zeros(bs + 3, dtype=np.int64)
+    S = g.integers(0, 40, bs)
+    pts = [g.permutation(n_pages) + 1000 * (i + 1) for i in range(bs)]   # disjoint page ids per request
+    loc = np.array([pts[i][(S[i] + r) // page] * page + (S[i] + r) % page for i in range(bs) for r in range(K)])
+    budgets = [int(x) for x in g.integers(-1, 2 * K, bs)]
+    stops = [set(int(x) for x in g.integers(0, 12, 2)) for _ in range(bs)]
+    vocabs = [int(x) for x in g.integers(5, 12, bs)]
+    packed, _, seq2, free, _, cut = ss_commit(predict, acc, a0, rpi, seeds, S, loc, K, page=page,
+                                              finish=(budgets, stops, vocabs))
+    want_free = []
+    for i in range(bs):
+        a = int(acc[i])
+        T = [int(a0[i])] + [int(predict[i * K + t]) for t in range(a + 1)]
+        j = a + 1 if budgets[i] < 0 else cut_index_loop(T, budgets[i], stops[i], vocabs[i])
+        assert cut[i] == j and seq2[i] == S[i] + j
+        kept_pages = {int(pts[i][p // page]) for p in range(int(S[i]) + j)}
+        want_free += [int(loc[i * K + r]) for r in range(K) if r >= j and int(loc[i * K + r]) // page not in kept_pages]
+    assert free.tolist() == want_free
 
 
 class _SP:
@@ -167,22 +193,19 @@ class _Req:
         self.hist.append(n)
 
 
-def test_product_host_commit_equals_oracle_loop():
-    from gravityocr_amd.selfspec_commit_rules import host_commit
-    g = np.random.default_rng(4)
-    for _ in range(300):
-        K = int(g.integers(2, 8))
-        n = int(g.integers(1, 5))
-        rows, budgets = [], []
-        reqs = []
-        for _ in range(n):
-            a = int(g.integers(0, K))
-            rows.append([int(g.integers(0, 12)), a] + [int(x) for x in g.integers(0, 12, K)])
-            mx = int(g.integers(1, 12))
-            reqs.append(_Req(mx, 10))
-            budgets.append(mx)
-        toks, js, accs = host_commit(reqs, rows)
-        otoks, ojs, oaccs = host_commit_loop(rows, budgets, [{3, 7}] * n, 10)
-        assert toks == otoks and js == ojs and accs == oaccs
-        for r, t in zip(reqs, toks):
-            assert r.output_ids == t
+@settings(max_examples=300, deadline=None)
+@given(st.lists(st.integers(-2, 12), min_size=1, max_size=10), st.integers(1, 12), st.integers(0, 5),
+       st.integers(5, 11))
+def test_cut_index_loop_equals_request_appends(T, max_new, prior, vocab):
+    """The oracle's per-token cut against a request object that appends T one token at a time and runs its own
+    finish check after each append (length, stop ids 3 and 7, vocabulary bound), starting from ``prior`` tokens."""
+    req = _Req(max_new + prior, vocab)
+    req.output_ids = [0] * prior
+    j = len(T) - 1
+    for t, x in enumerate(T):
+        req.output_ids.append(x)
+        req.check_finished()
+        if req.finished():
+            j = t
+            break
+    assert cut_index_loop(T, max_new, {3, 7}, vocab) == j
