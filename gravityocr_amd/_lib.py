@@ -21,6 +21,7 @@ SIGNATURES = {
     "gss_verify_attn": ([_p, _p, _p, _p, _i, _p, _i, _p, _p, _p, _i, _i, _i, _i, _i, _i, _f, _p, _p, _sz, _p], _i),
     "gss_argmax_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_argmax_accept": ([_p, _i, _i64, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
+    "gss_argmax_accept_noalloc": ([_p, _i, _i64, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p], _i),
     "gss_unmask_workspace_size": ([_i, _i, _i, _psz], _i),
     "gss_unmask_step": ([_p, _i, _i64, _i, _i, _i, _p, _i, _f, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
     "gss_kv_commit_workspace_size": ([_i, _psz], _i),

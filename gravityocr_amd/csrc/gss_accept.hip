@@ -9,6 +9,8 @@
 //   It then resets the counter, so the workspace needs zeroing only once and the launch is graph-replayable.
 #include "gss_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int ARG_THREADS = 256;
@@ -247,6 +249,88 @@ extern "C" int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, 
   p.part = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + PARTS_OFFSET);
   const dim3 grid(p.n_chunks, bs * W);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == GSS_BF16)
+    hipLaunchKernelGGL(argmax_accept_kernel<uint16_t>, grid, dim3(ARG_THREADS), 0, st, p);
+  else
+    hipLaunchKernelGGL(argmax_accept_kernel<float>, grid, dim3(ARG_THREADS), 0, st, p);
+  return gss_launch_status();
+}
+
+// ---------------------------------------------------------------- argmax + accept without allocation -----------
+// gss_argmax_accept_noalloc: the same kernel on a scratch block compiled into the library, for callers that cannot
+// allocate. `scratch` is a file-scope device array (each GPU holds its own copy for the life of the process); host
+// code never passes its name to a kernel (in host code the name is a stand-in, not a device address): the device
+// address comes from hipGetSymbolAddress, once per device, with that device current, and only that address is
+// used. Layout: the arrival counters of NOALLOC_MAX_SEQ sequences, then the chunk winners of up to
+// NOALLOC_MAX_SEQ * MAX_W rows of MAX_CHUNKS chunks (1,122,304 bytes in all).
+namespace {
+constexpr int NOALLOC_MAX_SEQ = 64;
+constexpr size_t NOALLOC_COUNTER_BYTES = static_cast<size_t>(NOALLOC_MAX_SEQ) * (SUB + 1) * LINE_U32 * sizeof(uint32_t);
+constexpr size_t NOALLOC_PART_BYTES = static_cast<size_t>(NOALLOC_MAX_SEQ) * MAX_W * MAX_CHUNKS * sizeof(uint64_t);
+constexpr size_t NOALLOC_SCRATCH_BYTES = NOALLOC_COUNTER_BYTES + NOALLOC_PART_BYTES;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+__global__ void __launch_bounds__(256) zero_words_kernel(uint32_t* p, size_t n) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    p[i] = 0u;
+}
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES];  // device address of `scratch` on each device (null: not set up yet)
+
+// The current device's scratch address. On the first call per device it is looked up and its arrival counters are
+// cleared by a fill kernel on `st` (ordered before the caller's launch on the same stream; the kernels leave the
+// counters at zero after every call, so this is the only clear).
+int noalloc_scratch(hipStream_t st, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= NOALLOC_MAX_DEVICES) return GSS_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || ptr == nullptr) return GSS_ERR_LAUNCH;
+    hipLaunchKernelGGL(zero_words_kernel, dim3(16), dim3(256), 0, st, static_cast<uint32_t*>(ptr),
+                       NOALLOC_COUNTER_BYTES / sizeof(uint32_t));
+    if (gss_launch_status() != GSS_OK) return GSS_ERR_LAUNCH;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GSS_OK;
+}
+
+}  // namespace
+
+extern "C" int gss_argmax_accept_noalloc(const void* logits, int dtype, int64_t ld_row, int bs, int W, int V,
+                                         int flags, const int32_t* window, int32_t* target, int32_t* accept_len,
+                                         int32_t* next_x0, int32_t* packed, gss_stream_t stream) {
+  if (!logits || !target || bs <= 0 || W <= 0 || V <= 0 || ld_row < V) return GSS_ERR_ARG;
+  if (dtype != GSS_BF16 && dtype != GSS_F32) return GSS_ERR_ARG;
+  if (flags & ~(GSS_ARGMAX_SOFTMAX | GSS_ARGMAX_LAST_RAW)) return GSS_ERR_ARG;
+  if (W > MAX_W || V > MAX_CHUNKS * CHUNK || bs > NOALLOC_MAX_SEQ) return GSS_ERR_UNSUPPORTED;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* base = nullptr;
+  const int rc = noalloc_scratch(st, &base);
+  if (rc != GSS_OK) return rc;
+  ArgParams p;
+  p.logits = logits;
+  p.ld_row = ld_row;
+  p.W = W;
+  p.V = V;
+  p.flags = flags;
+  p.n_chunks = (V + CHUNK - 1) / CHUNK;
+  p.window = window;
+  p.target = target;
+  p.accept_len = accept_len;
+  p.next_x0 = next_x0;
+  p.packed = packed;
+  p.counters = static_cast<uint32_t*>(base);
+  p.part = reinterpret_cast<uint64_t*>(static_cast<char*>(base) + NOALLOC_COUNTER_BYTES);
+  const dim3 grid(p.n_chunks, bs * W);
   if (dtype == GSS_BF16)
     hipLaunchKernelGGL(argmax_accept_kernel<uint16_t>, grid, dim3(ARG_THREADS), 0, st, p);
   else

@@ -136,6 +136,26 @@ def argmax_accept(logits, target, workspace, *, window=None, accept_len=None, ne
                                   workspace.numel() * workspace.element_size(), _stream()), "gss_argmax_accept")
 
 
+def argmax_accept_noalloc(logits, target, *, window=None, accept_len=None, next_x0=None, packed=None,
+                          flags: int = 0):
+    """argmax_accept without a workspace (gss_argmax_accept_noalloc: the library's own scratch, nothing allocated);
+    bs <= 64. Same arguments and outputs as argmax_accept."""
+    bs, W, V = logits.shape
+    if not logits.is_cuda or logits.stride(2) != 1 or logits.stride(0) != W * logits.stride(1):
+        raise ValueError("logits must be a GPU tensor [bs, W, V] with dense rows and a uniform row stride")
+    dt = {torch.bfloat16: 0, torch.float32: 1}.get(logits.dtype)
+    if dt is None:
+        raise ValueError("logits must be bf16 or fp32")
+    _need(target, torch.int32, "target", (bs, W))
+    for name, t, shp in (("window", window, (bs, W)), ("accept_len", accept_len, (bs,)),
+                         ("next_x0", next_x0, (bs,)), ("packed", packed, (bs, W + 2))):
+        if t is not None:
+            _need(t, torch.int32, name, shp)
+    check(lib().gss_argmax_accept_noalloc(_ptr(logits), dt, logits.stride(1), bs, W, V, int(flags), _ptr(window),
+                                          _ptr(target), _ptr(accept_len), _ptr(next_x0), _ptr(packed), _stream()),
+          "gss_argmax_accept_noalloc")
+
+
 def unmask_workspace_bytes(bs, W, V) -> int:
     n = ctypes.c_size_t(0)
     check(lib().gss_unmask_workspace_size(bs, W, V, ctypes.byref(n)), "gss_unmask_workspace_size")

@@ -127,6 +127,17 @@ int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, int bs, int
                       const int32_t* window, int32_t* target, int32_t* accept_len, int32_t* next_x0, int32_t* packed,
                       void* workspace, size_t workspace_bytes, gss_stream_t stream);
 
+/* gss_argmax_accept_noalloc: gss_argmax_accept (same arguments and outputs, bit for bit) with no workspace argument
+ * and no allocation of any kind. No counterpart in the reference: it is for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Its scratch (arrival counters and chunk
+ * winners, 1,122,304 bytes) is a device array inside the library: each GPU the library runs on holds one copy
+ * until the process ends, set up on the first call on that device (the current device). Limits: bs <= 64,
+ * W <= 64, V <= 131072 (GSS_ERR_UNSUPPORTED beyond them). Every call on one GPU shares that GPU's scratch: calls
+ * that overlap on one GPU (different streams, or host threads) race; calls ordered on one stream do not. */
+int gss_argmax_accept_noalloc(const void* logits, int dtype, int64_t ld_row, int bs, int W, int V, int flags,
+                              const int32_t* window, int32_t* target, int32_t* accept_len, int32_t* next_x0,
+                              int32_t* packed, gss_stream_t stream);
+
 /* ---------------------------------------------------------------- block-diffusion unmask step -------------------
  * Replaces one iteration of the threshold-unmask loop of the cached block-diffusion decode at temperature 0
  * (src/fast_sampling.py:206-216 generate_cached; src/fast_sampling_batched.py:198-211 generate_cached_batched):
