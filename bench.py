@@ -29,6 +29,31 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
+def cpu_info():
+    """The host's CPU model and its physical cores and logical threads (lscpu's fields, read from /proc/cpuinfo)."""
+    model, cores = None, set()
+    try:
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+        if phys is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    return {"cpu_model": model, "physical_cores": len(cores) or None, "logical_threads": os.cpu_count(),
+            "torch_threads": torch.get_num_threads()}
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -98,6 +123,125 @@ def attn_batched_roofline(dev, W=17, bs=32, copies=2, Hq=16, Hkv=2, D=128, seed=
     return us, nbytes, flops
 
 
+def argmax_roofline(dev, b, W=17, V=59392):
+    """gss_argmax_accept at the accept shape: bf16 logits [b, W, V] (b * W * V * 2 bytes) with the window, accept,
+    next boundary token and packed row outputs, cycled over enough distinct logits buffers (> 256 MB together) that
+    they come from HBM. Returns (microseconds per call, algorithmic bytes per call)."""
+    from gravityocr_amd import kernels as K
+    nbytes = b * W * V * 2
+    copies = max(2, -(-(320 << 20) // nbytes))
+    g = torch.Generator(device=dev).manual_seed(11)
+    lg = torch.randn(copies, b, W, V, device=dev, generator=g).bfloat16()
+    win = torch.randint(0, V, (b, W), device=dev, generator=g, dtype=torch.int32)
+    tgt = torch.empty(b, W, dtype=torch.int32, device=dev)
+    acc, x0 = (torch.empty(b, dtype=torch.int32, device=dev) for _ in range(2))
+    packed = torch.empty(b, W + 2, dtype=torch.int32, device=dev)
+    ws = torch.zeros(K.argmax_workspace_bytes(b, W, V), dtype=torch.uint8, device=dev)
+    fns = [lambda i=i: K.argmax_accept(lg[i], tgt, ws, window=win, accept_len=acc, next_x0=x0, packed=packed)
+           for i in range(copies)]
+    return time_kernel(fns, n=max(1, 256 // copies)), nbytes
+
+
+def commit_roofline(dev, n_rows=17, L=8448, layers=16, Hkv=2, D=128, reps=5, n=64):
+    """gss_kv_commit of a whole verify window at bs = 1 (the 16-layer decoder's staging, all n_rows rows kept) into
+    16-token pages at prefix L. Algorithmic bytes: the rows read from the staging and written to the pages, K and V,
+    every layer. The n calls of a timed graph append n windows (the length is reset between replays, outside the
+    timed region). Returns (microseconds per call, algorithmic bytes per call)."""
+    from gravityocr_amd import kernels as K
+    cap = L + (n + 2) * n_rows + 64
+    ppseq = (cap + 15) // 16
+    g = torch.Generator(device=dev).manual_seed(12)
+    kw = torch.randn(layers, 1, n_rows, Hkv, D, device=dev, generator=g).bfloat16()
+    vw = torch.randn_like(kw)
+    kp = torch.zeros(layers, ppseq, Hkv, 16, D, dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros(layers, ppseq, Hkv, D, 16, dtype=torch.bfloat16, device=dev)
+    pt = torch.randperm(ppseq, device=dev, generator=g).int().view(1, -1)
+    sl = torch.tensor([L], dtype=torch.int32, device=dev)
+    ws = torch.zeros(K.commit_workspace_bytes(1), dtype=torch.uint8, device=dev)
+    K.kv_commit(kw, vw, kp, vp, pt, sl, ws, n_add=n_rows)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    sl.fill_(L)
+    with torch.cuda.graph(gr):
+        for _ in range(n):
+            K.kv_commit(kw, vw, kp, vp, pt, sl, ws, n_add=n_rows)
+    total = 0.0
+    for _ in range(reps):
+        sl.fill_(L)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        total += e0.elapsed_time(e1)
+    return total * 1e3 / (reps * n), 2 * 2 * layers * n_rows * Hkv * D * 2
+
+
+def batched_rounds(dev, w, cfg, block_sizes=(8, 16, 32), rounds=256, bs=32, seed=3):
+    """The batched serving shape: bs sequences with prefixes L_i ~ U[1024, 12288] (seed 3) in one shuffled pool of
+    16-token pages, prefix K/V seeded N(0, 0.8) (the spread of this model's projected K/V; the kernels' cost does not
+    depend on the values), each sequence's x0 a seeded random id. For each block size: ``rounds`` graph-replayed
+    full-draft rounds of the whole batch (every sequence its own accept length), and as many graph-replayed AR steps
+    of the batch. Returns a dict per block size."""
+    from gravityocr_amd.engine import GssEngine, SelfSpecDecoder
+    rng = np.random.default_rng(seed)
+    L0 = rng.integers(1024, 12289, size=bs)
+    max_bd = max(block_sizes)
+    eng = GssEngine(cfg, w, max_bs=bs, max_len=int(L0.max()) + rounds * (max_bd + 2) + 2 * (max_bd + 2) + 64,
+                    device=dev, page_seed=seed, max_win=max_bd + 2)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    eng.k_pages.normal_(0.0, 0.8, generator=g)
+    eng.v_pages.normal_(0.0, 0.8, generator=g)
+    x0 = torch.tensor(rng.integers(0, cfg.vocab - 1, size=bs), dtype=torch.int32, device=dev)
+    L0_dev = torch.tensor(L0, dtype=torch.int32, device=dev)
+    out = {}
+    for bd in block_sizes:
+        dec = SelfSpecDecoder(eng, bd=bd, mask_id=cfg.vocab - 1, bs=bs, max_rounds=rounds + 8)
+
+        def reset():
+            eng.seq_lens[:bs].copy_(L0_dev)
+            dec.start(x0)
+
+        reset()
+        dec.round()
+        reset()
+        dec.ar_step()
+        reset()
+        dec.capture()
+        reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(rounds):
+            dec.g_round.replay()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        accs = dec.accept_lengths(rounds)                                   # [rounds, bs]
+        n_commit = int((accs + 2).sum())
+        reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(rounds):
+            dec.g_ar.replay()
+        torch.cuda.synchronize()
+        adt = time.perf_counter() - t0
+        per_seq = [np.bincount(accs[:, b], minlength=bd + 1).tolist() for b in range(bs)]
+        out[str(bd)] = {"K": bd + 1, "rounds": rounds, "round_us": round(dt / rounds * 1e6, 1),
+                        "committed_tokens": n_commit, "tokens_per_s": round(n_commit / dt, 1),
+                        "ar_step_us": round(adt / rounds * 1e6, 1), "ar_tokens_per_s": round(bs * rounds / adt, 1),
+                        "speedup_vs_ar": round((n_commit / dt) / (bs * rounds / adt), 3),
+                        "mean_committed_per_round_per_seq": round(n_commit / (rounds * bs), 3),
+                        "accept_hist": np.bincount(accs.reshape(-1), minlength=bd + 1).tolist(),
+                        "accept_hist_per_seq": per_seq}
+        log(f"batched B={bd}: {out[str(bd)]['round_us']} us/round, {out[str(bd)]['tokens_per_s']} tokens/s, "
+            f"AR {out[str(bd)]['ar_tokens_per_s']} tokens/s")
+        del dec
+    out["prefixes"] = {"min": int(L0.min()), "max": int(L0.max()), "sum": int(L0.sum())}
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def copy_calibration(dev, reps=3):
     """Plain device copies of COPY_BYTES, as an elementwise kernel (reads COPY_BYTES, writes COPY_BYTES): the
     calibration kernel of the FETCH_SIZE / WRITE_SIZE passes."""
@@ -163,6 +307,12 @@ def main():
                     help="only the draft-attention roofline measurement and the copy calibration (for rocprof runs)")
     ap.add_argument("--attn-batched-only", action="store_true",
                     help="only the batched (32 ragged sequences) draft-attention measurement (for rocprof runs)")
+    ap.add_argument("--batched-only", action="store_true",
+                    help="only the batched rounds (32 ragged sequences, B in 8/16/32) (for rocprof runs)")
+    ap.add_argument("--no-batched", action="store_true", help="skip the batched rounds")
+    ap.add_argument("--batched-rounds", type=int, default=256)
+    ap.add_argument("--small-only", action="store_true",
+                    help="only the argmax / accept and KV-commit measurements (for rocprof runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the self-spec round shards by sequence (no collective), so a multi-GPU "
@@ -192,12 +342,20 @@ def main():
     from gravityocr_amd import kernels as K
 
     dev = torch.device("cuda:0")
+    if args.small_only:
+        res = {"argmax": {str(b): round(argmax_roofline(dev, b)[0], 2) for b in (1, 8, 32)},
+               "kv_commit_us": round(commit_roofline(dev)[0], 2)}
+        print(json.dumps(res), flush=True)
+        return
     bd, Kw, P = args.bd, args.bd + 1, args.prefix
     t0 = time.time()
     w = synthetic_weights(cfg, seed=2)
     vis, ids = synthetic_prompt(cfg, 2048, P - 2048, seed=2)
     emb = torch.cat([vis, w["embed"][ids]], 0)
     log(f"weights + prompt drawn in {time.time() - t0:.1f}s")
+    if args.batched_only:
+        print(json.dumps(batched_rounds(dev, w, cfg, rounds=args.batched_rounds)), flush=True)
+        return
     max_len = P + args.tokens + 4 * (Kw + 1) + 64
     eng = GssEngine(cfg, w, max_bs=1, max_len=max_len, device=dev)
     mask_id = cfg.vocab - 1
@@ -380,6 +538,22 @@ def main():
     log(f"batched draft attention (32 ragged sequences): {b_us:.2f} us, {b_bytes / (b_us * 1e-6) / 1e9:.0f} GB/s; "
         f"by block size {by_block}")
 
+    # ---- argmax / accept and KV commit at the round's shapes ---------------------------------------------------
+    small = {"argmax": {}, "kv_commit": None}
+    for b in (1, 8, 32):
+        u, nb = argmax_roofline(dev, b)
+        small["argmax"][str(b)] = {"avg_us": round(u, 2), "bytes": nb, "GBs": round(nb / (u * 1e-6) / 1e9, 1),
+                                   "frac": round(nb / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    u, nb = commit_roofline(dev, n_rows=Kw, L=L)
+    small["kv_commit"] = {"avg_us": round(u, 2), "bytes": nb, "rows": Kw, "GBs": round(nb / (u * 1e-6) / 1e9, 1),
+                          "frac": round(nb / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"argmax / accept and KV commit: {small}")
+
+    # ---- batched serving shape: 32 ragged sequences, B in {8, 16, 32} --------------------------------------------
+    batched = None
+    if not args.no_batched and not args.profile_only:
+        batched = batched_rounds(dev, w, cfg, rounds=args.batched_rounds)
+
     # ---- CPU baseline: the oracle's round on the host cores, from the same 8K state -----------------------------
     cpu = None
     if not args.no_cpu and not args.profile_only:
@@ -410,7 +584,7 @@ def main():
         cdt = time.perf_counter() - t0
         cpu = {"value": round(n_t / cdt, 3), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
                "sample": f"{n_r} full-draft rounds (B={bd}) of the fp32 oracle from the same {P}-token state, "
-                         f"{cdt:.1f}s", "round_ms": round(cdt / n_r * 1e3, 1)}
+                         f"{cdt:.1f}s", "round_ms": round(cdt / n_r * 1e3, 1), **cpu_info()}
         log(f"CPU baseline: {cpu}")
 
     round_bytes = 2 * (1_088_618_496 + 16 * 1024 * (L + Kw) + Kw * cfg.vocab * 2)
@@ -420,8 +594,9 @@ def main():
         "ms_per_step": round(round_us / 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16", "data": "synthetic (random-init weights, seeded N(0,1) visual embeddings and U[0,V) ids)",
         "config": {"workload": f"bs=1 self-spec full-draft rounds, 16-layer 1536-hidden GLM decoder, {P}-token "
-                               f"prefix, B={bd}, {args.tokens} committed tokens", "bs": 1, "prefix": P, "bd": bd,
-                   "K": Kw, "tokens": args.tokens, "parallelism": "none (one GPU)"},
+                               f"prefix, B={bd}: {steps} timed rounds committing {n_commit} tokens",
+                   "bs": 1, "prefix": P, "bd": bd, "K": Kw, "timed_rounds": steps, "timed_tokens": n_commit,
+                   "parallelism": "none (one GPU)"},
         "round_us": round(round_us, 1),
         "mean_committed_per_round": round(n_commit / steps, 3),
         "accept_hist": np.bincount(accs, minlength=bd + 1).tolist(),
@@ -447,6 +622,9 @@ def main():
                              "mfma_tflops": round(b_flops / (b_us * 1e-6) / 1e12, 1),
                              "mfma_frac": round(b_flops / (b_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                              "by_block_size": by_block},
+        "argmax_accept": small["argmax"],
+        "kv_commit": small["kv_commit"],
+        "batched": batched,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

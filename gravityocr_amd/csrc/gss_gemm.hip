@@ -1,8 +1,7 @@
 // Skinny GEMM for the decode forwards: Y[M, N] = X[M, Kd] . W[N, Kd]^T with M = bs * window rows, bf16 operands,
 // fp32 accumulation. Weight streaming is the whole cost at M <= 64 (N*Kd*2 bytes per call), so the kernel is built
 // to keep many 16-byte weight loads in flight and to touch every weight byte exactly once. Batched windows (M > 64)
-// run as slabs of 64 rows: one workgroup per (column tile, slab), the slabs of a tile back to back on one XCD so
-// they share its weights through that XCD's L2.
+// run on a tiled kernel (gemm_tiled_kernel) that computes every element with the same sequence of operations.
 //
 // Layout on v_mfma_f32_16x16x32_bf16: A = 16 weight rows x 32 k (lane: row l%16, k 8*(l/16)..+7, one 16-byte
 // load), B = 32 k x 16 activation rows (lane: activation row l%16, same k), C = Y^T tile (lane: 4 consecutive
@@ -10,9 +9,8 @@
 // contiguous ranges and reduce their partial tiles through LDS in wave order.
 //
 // Batch invariance: an output element is always the same sequence of MFMA k-steps and the same wave-order
-// reduction, whatever M is and wherever its row sits (in which slab, at which row of it), so a row computed in a
-// 17-row verify forward or a 544-row batched verify is bit-identical to the same row computed alone (a 1-row AR
-// step). Decode parity between speculative and AR decoding rests on it.
+// reduction, whatever M is, whichever kernel runs it and wherever its row sits, so a row computed in a 17-row verify
+// forward or a 544-row batched verify is bit-identical to the same row computed alone (a 1-row AR step). Decode parity between speculative and AR decoding rests on it.
 //
 // Fused epilogues (the GEMM output is rounded to bf16 first, as a bf16 torch linear writes it):
 //   EPI_PLAIN   Y bf16 (or fp32) [M, ldy]
@@ -66,26 +64,7 @@ struct GemmParams {
   uint16_t* post_x;
   float post_eps;
   uint32_t* done_ctr;
-  // row slabs: M > 64 rows run as n_slabs slabs of up to 64 rows, one workgroup per (column tile, slab), each
-  // computing exactly what a call with the slab's rows alone computes (tile_slab gives the mapping)
-  int n_slabs;
-  int slab_xcd;  // 1: the slabs of one column tile run back to back on one XCD (needs n_tiles % 8 == 0)
 };
-
-// Column tile and row slab of workgroup x of gemm_kernel. Workgroups are dealt to the 8 XCDs round-robin by linear
-// index; with slab_xcd the n_slabs slabs of a column tile get consecutive indices on one XCD (x % 8 == tile % 8), so
-// the later slabs read the tile's weights from that XCD's L2 instead of HBM.
-struct TileSlab {
-  int tile, slab;
-};
-GSS_DEV TileSlab tile_slab(const GemmParams& p, int x) {
-  if (p.n_slabs == 1) return {x, 0};
-  if (p.slab_xcd) {
-    const int j = x / 8;
-    return {(j / p.n_slabs) * 8 + x % 8, j % p.n_slabs};
-  }
-  return {x / p.n_slabs, x % p.n_slabs};
-}
 
 constexpr int MAX_NW = 12;  // waves per workgroup (768 threads: 168 VGPRs per lane)
 constexpr size_t MAX_LDS = 160 * 1024;  // LDS per workgroup on gfx950
@@ -311,11 +290,9 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   extern __shared__ floatx4_t red[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
-  const TileSlab ts = tile_slab(p, blockIdx.x);
-  const int f0 = ts.tile * FT * 16;
-  // this workgroup's rows: [row0, row0 + Ms); everything below sees only them (x, the staging, the epilogue)
-  const int row0 = ts.slab * 64, Ms = min(64, p.M - row0);
-  const uint16_t* xs0 = p.x + static_cast<int64_t>(row0) * p.ldx;
+  const int f0 = blockIdx.x * FT * 16;
+  const int row0 = 0, Ms = p.M;  // every row (M <= 64)
+  const uint16_t* xs0 = p.x;
   const int ksteps = p.Kd / 32;
   const int ks = blockIdx.y;  // k split: k-steps [ks * kps, (ks + 1) * kps)
   const int k_end = min(ksteps, (ks + 1) * p.kps);
@@ -627,7 +604,7 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
 // it is a function of the weight shape (and the device's CU count) only: it fixes the reduction order, so it is a
 // constant, never a setting that could differ between two calls on the same weights.
 constexpr int MAX_KSPLIT = 2;
-constexpr int MAX_ROWS = 65536;  // rows of one call (slabs of 64)
+constexpr int MAX_ROWS = 65536;  // rows of one call
 constexpr bool kStageX = true;  // stage the activations through LDS where it applies (gemm_kernel)
 
 // Dynamic LDS beyond the default 64 KB for kernel K (once per process, before its first launch).
@@ -681,20 +658,210 @@ size_t gemm_ws_bytes(int M, int N, int Kd) {
   return CTR_BYTES + (ks > 1 ? static_cast<size_t>(ks) * M * N * sizeof(float) : 0);
 }
 
+// ---- batched windows (M > 64): a tiled kernel with gemm_kernel's arithmetic ---------------------------------------
+// Each output element of gemm_kernel is, for every k split ks (in order), the left fold over the waves v = 0..nw-1 of
+// P_v = the MFMA chain (v_mfma_f32_16x16x32_bf16, weights as A, activations as B, accumulating from zero) over the
+// k-steps [ks*kps + v*ksw, ks*kps + (v+1)*ksw) clipped to the split; the splits are then written as parts or
+// folded in split order. This kernel computes exactly that sequence of operations per element, but with a GEMM
+// tiling: a workgroup owns a BF-feature x BM-row block, its 4 waves a WF x WN grid of 16x16 tiles each, and every
+// wave walks all k-steps of the split itself, restarting its accumulator P at each wave-range boundary (ksw k-steps,
+// a multiple of the 4-k-step LDS chunk) and folding it into S. Weights and activations stream through two LDS
+// buffers of 4 k-steps (direct-to-LDS loads, the next chunk in flight while the current one is computed), rows
+// XOR-swizzled by 16-byte chunk so the 16 rows of a fragment read hit distinct banks. Every weight byte is read
+// once per row block instead of once per 64 rows, and every activation byte once per feature block.
+constexpr int TK = 4;    // k-steps per LDS chunk
+constexpr int TCH = 16;  // 16-byte chunks per LDS row (TK * 32 bf16)
+
+GSS_DEV void dma16_lds(const void* g, const void* lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
+}
+
+template <int EPI, int WF, int WN>
+__global__ void __launch_bounds__(256) gemm_tiled_kernel(GemmParams p, int ksw) {
+  constexpr int BF = 2 * WF * 16, BM = 2 * WN * 16, ROWS = BF + BM;
+  constexpr int PER_WAVE = ROWS * TCH / 64 / 4;  // direct-to-LDS instructions per wave per chunk
+  extern __shared__ __attribute__((aligned(16))) u32x4_t tl[];  // [2][ROWS][TCH]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wf = wv & 1, wn = wv >> 1;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const int fb = blockIdx.x * BF, rb = blockIdx.y * BM;
+  const int ksteps = p.Kd / 32;
+  // splits this workgroup computes: one (EPI_PARTS: blockIdx.z) or all of them, folded in split order
+  const int ks_lo = EPI == EPI_PARTS ? static_cast<int>(blockIdx.z) : 0;
+  const int ks_hi = EPI == EPI_PARTS ? ks_lo + 1 : p.ksplit;
+  // chunk list: split by split, TK k-steps each from the split's first k-step (the last chunk of a split may be
+  // shorter); wave-range boundaries fall on chunk starts because ksw is a multiple of TK
+  auto split_beg = [&](int ks) { return ks * p.kps; };
+  auto split_end = [&](int ks) { return min(ksteps, (ks + 1) * p.kps); };
+  int n_chunks = 0;
+  for (int ks = ks_lo; ks < ks_hi; ++ks) n_chunks += (max(0, split_end(ks) - split_beg(ks)) + TK - 1) / TK;
+
+  // chunk i -> (split, first k-step, k-steps): walked in order, so keep a cursor
+  auto issue = [&](int ks, int s0, int buf) {
+    const int kend = split_end(ks);
+    u32x4_t* base = tl + buf * ROWS * TCH;
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int slot = (j * 4 + wv) * 64 + lane;  // slot of this lane's 16 bytes in the chunk's LDS image
+      const int r = slot / TCH, cp = slot % TCH;  // LDS row, physical chunk
+      const int c = cp ^ (r & 15);                // the logical chunk stored there
+      const int s = min(s0 + c / 4, kend - 1);    // its k-step (past the split: a repeat, never used)
+      const uint16_t* src;
+      if (r < BF) {
+        const int f = min(fb + r, p.N - 1);
+        src = p.w + static_cast<int64_t>(f) * p.ldw + s * 32 + (c % 4) * 8;
+      } else {
+        const int m = min(rb + r - BF, p.M - 1);
+        src = p.x + static_cast<int64_t>(m) * p.ldx + s * 32 + (c % 4) * 8;
+      }
+      dma16_lds(src, base + (j * 4 + wv) * 64);
+    }
+  };
+
+  floatx4_t P[WF][WN], S[WF][WN], T[WF][WN];
+  auto zero = [](floatx4_t(&a)[WF][WN]) {
+#pragma unroll
+    for (int f = 0; f < WF; ++f)
+#pragma unroll
+      for (int n = 0; n < WN; ++n) a[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  zero(P);
+  zero(S);
+  zero(T);
+  const int fr0 = wf * WF * 16 + l16;          // this lane's A row (feature) in the block, tile 0
+  const int mr0 = BF + wn * WN * 16 + l16;     // its B row (activation) in the LDS image, tile 0
+
+  int ks = ks_lo, s0 = split_beg(ks), v_done = 0;  // cursor: split, chunk start, waves folded into S
+  bool s_set = false;
+  // the first chunk
+  {
+    int kq = ks, sq = s0;
+    while (kq < ks_hi && sq >= split_end(kq)) sq = split_beg(++kq);
+    ks = kq;
+    s0 = sq;
+    if (ks < ks_hi) issue(ks, s0, 0);
+  }
+  for (int i = 0; i < n_chunks; ++i) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int kend = split_end(ks), nk = min(TK, kend - s0);
+    // the next chunk's position, then its loads into the other buffer (read by every wave two chunks ago)
+    int ks_n = ks, s_n = s0 + TK;
+    if (s_n >= kend) {
+      ks_n = ks + 1;
+      s_n = ks_n < ks_hi ? split_beg(ks_n) : 0;
+    }
+    if (i + 1 < n_chunks) issue(ks_n, s_n, (i + 1) & 1);
+    // a wave-range boundary at this chunk's start: fold P into S
+    if (s0 != split_beg(ks) && (s0 - split_beg(ks)) % ksw == 0) {
+#pragma unroll
+      for (int f = 0; f < WF; ++f)
+#pragma unroll
+        for (int n = 0; n < WN; ++n) {
+          S[f][n] = s_set ? S[f][n] + P[f][n] : P[f][n];
+          P[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      s_set = true;
+      ++v_done;
+    }
+    const u32x4_t* buf = tl + (i & 1) * ROWS * TCH;
+#pragma unroll
+    for (int u = 0; u < TK; ++u) {
+      if (u < nk) {  // workgroup-uniform
+        bf16x8_t a[WF], b[WN];
+#pragma unroll
+        for (int f = 0; f < WF; ++f)
+          a[f] = __builtin_bit_cast(bf16x8_t, buf[(fr0 + f * 16) * TCH + ((u * 4 + g4) ^ l16)]);
+#pragma unroll
+        for (int n = 0; n < WN; ++n)
+          b[n] = __builtin_bit_cast(bf16x8_t, buf[(mr0 + n * 16) * TCH + ((u * 4 + g4) ^ l16)]);
+#pragma unroll
+        for (int f = 0; f < WF; ++f)
+#pragma unroll
+          for (int n = 0; n < WN; ++n) P[f][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[f], b[n], P[f][n], 0, 0, 0);
+      }
+    }
+    if (s0 + TK >= kend) {
+      // the split's last chunk: fold the last wave range, then the empty ones of gemm_kernel's last split (+0.0
+      // each: only the sign of a zero can change), then the split's sum
+      const int nw = (p.kps + ksw - 1) / ksw;
+#pragma unroll
+      for (int f = 0; f < WF; ++f)
+#pragma unroll
+        for (int n = 0; n < WN; ++n) {
+          S[f][n] = s_set ? S[f][n] + P[f][n] : P[f][n];
+          if (v_done + 1 < nw) S[f][n] = S[f][n] + floatx4_t{0.f, 0.f, 0.f, 0.f};
+          P[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      if constexpr (EPI == EPI_PARTS) {
+#pragma unroll
+        for (int f = 0; f < WF; ++f)
+#pragma unroll
+          for (int n = 0; n < WN; ++n) {
+            const int row = rb + wn * WN * 16 + n * 16 + l16, feat = fb + wf * WF * 16 + f * 16 + g4 * 4;
+            if (row < p.M && feat < p.N)
+              *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) +
+                                            (static_cast<int64_t>(ks) * p.M + row) * p.ldy + feat) = S[f][n];
+          }
+      } else {
+#pragma unroll
+        for (int f = 0; f < WF; ++f)
+#pragma unroll
+          for (int n = 0; n < WN; ++n) T[f][n] = ks == ks_lo ? S[f][n] : T[f][n] + S[f][n];
+      }
+      s_set = false;
+      v_done = 0;
+    }
+    ks = ks_n;
+    s0 = s_n;
+  }
+  if constexpr (EPI != EPI_PARTS) {
+#pragma unroll
+    for (int f = 0; f < WF; ++f)
+#pragma unroll
+      for (int n = 0; n < WN; ++n) {
+        const int row = rb + wn * WN * 16 + n * 16 + l16, feat = fb + wf * WF * 16 + f * 16 + g4 * 4;
+        if (row < p.M && feat < p.N)
+          gemm_epilogue<EPI, false>(p, fb + wf * WF * 16, rb + wn * WN * 16, f, n, T[f][n], l16, g4);
+      }
+  }
+}
+
+template <int EPI, int WF, int WN>
+int launch_tiled_wf(GemmParams& p, int ksw, hipStream_t st) {
+  constexpr int BF = 2 * WF * 16, BM = 2 * WN * 16;
+  constexpr size_t lds = 2ull * (BF + BM) * TCH * sizeof(u32x4_t);
+  constexpr auto kern = gemm_tiled_kernel<EPI, WF, WN>;
+  if constexpr (lds > 64 * 1024) {
+    if (!allow_full_lds<kern>()) return GSS_ERR_LAUNCH;
+  }
+  const dim3 grid((p.N + BF - 1) / BF, (p.M + BM - 1) / BM, EPI == EPI_PARTS ? p.ksplit : 1);
+  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, p, ksw);
+  return gss_launch_status();
+}
+
+// The tiled kernel for M > 64: 128 x 128 blocks when they make at least ~one workgroup per CU, else 64 x 64 (any
+// tiling computes the same bits; only the speed depends on it). p.ksplit / p.kps / the wave range ksw are gemm_kernel's
+// for the same (N, Kd).
+template <int EPI>
+int launch_tiled(GemmParams& p, int ksw, hipStream_t st) {
+  const int64_t big = static_cast<int64_t>((p.N + 127) / 128) * ((p.M + 127) / 128) *
+                      (EPI == EPI_PARTS ? p.ksplit : 1);
+  if (big >= stream_wgs()) return launch_tiled_wf<EPI, 4, 4>(p, ksw, st);
+  return launch_tiled_wf<EPI, 2, 2>(p, ksw, st);
+}
+
 template <int FT, int NT, int EPI, int PRO, bool POST>
 int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
   const int ksteps = p.Kd / 32;
   const int n_tiles = (p.N + FT * 16 - 1) / (FT * 16);
   p.ksplit = EPI == EPI_PARTS ? gemm_parts_split(n_tiles, ksteps) : gemm_ksplit(n_tiles, ksteps);
   p.kps = (ksteps + p.ksplit - 1) / p.ksplit;
-  // rows beyond 64: slabs of 64 rows, each its own workgroup per column tile (the fused prologue and post-norm need
-  // every row in one workgroup, so they stay at M <= 64)
-  p.n_slabs = (p.M + 63) / 64;
-  p.slab_xcd = p.n_slabs > 1 && n_tiles % 8 == 0;
-  const int Mw = min(p.M, 64);  // rows of one workgroup
-  if ((PRO == PRO_ADDNORM || POST) && p.n_slabs > 1) return GSS_ERR_UNSUPPORTED;
+  const int Mw = p.M;  // rows of one workgroup (M <= 64 here)
   if ((p.ksplit > 1 && EPI != EPI_PARTS) || POST) {
-    if (static_cast<int64_t>(n_tiles) * p.n_slabs > CTR_TILES) return GSS_ERR_UNSUPPORTED;
+    if (n_tiles > CTR_TILES) return GSS_ERR_UNSUPPORTED;
     const size_t need = CTR_BYTES + (p.ksplit > 1 ? static_cast<size_t>(p.ksplit) * p.M * p.N * sizeof(float) : 0);
     if (!ws || ws_bytes < need) return GSS_ERR_WORKSPACE;
     p.tile_ctr = static_cast<uint32_t*>(ws);
@@ -705,7 +872,7 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
   int ksw = (p.kps + MAX_NW - 1) / MAX_NW;
   ksw = (ksw + 3) / 4 * 4;
   const int nw = (p.kps + ksw - 1) / ksw;
-  const dim3 grid(n_tiles * p.n_slabs, p.ksplit), block(64 * nw);
+  const dim3 grid(n_tiles, p.ksplit), block(64 * nw);
   size_t lds = static_cast<size_t>(nw) * FT * NT * 64 * sizeof(floatx4_t);
   if constexpr (PRO == PRO_ADDNORM) {
     lds += static_cast<size_t>(p.M) * (p.Kd + XPAD) * sizeof(uint16_t);
@@ -735,7 +902,7 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
       // more column tiles than CUs and one load pass per tile (a function of N and Kd only, so every row count
       // takes the same kernel): the persistent kernel, one workgroup per CU walking the tiles
       const int G = stream_wgs();
-      if (EPI != EPI_PARTS && p.ksplit == 1 && ksw <= 4 && n_tiles > G && p.n_slabs == 1) {
+      if (EPI != EPI_PARTS && p.ksplit == 1 && ksw <= 4 && n_tiles > G) {
         hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI>), dim3(G), block, lds, st, p, ksw, n_tiles);
         return gss_launch_status();
       }
@@ -768,7 +935,22 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
 
 template <int EPI, int PRO, bool POST>
 int launch_epi(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
-  const int NT = (min(p.M, 64) + 15) / 16;  // row tiles of one workgroup (one 64-row slab)
+  if (p.M > 64) {
+    // batched windows: the tiled kernel with the same k partition (splits and wave ranges of gemm_kernel for this
+    // (N, Kd)); the fused prologue and post-norm need every row in one workgroup, so they stay at M <= 64
+    if constexpr (PRO != PRO_NONE || POST) {
+      return GSS_ERR_UNSUPPORTED;
+    } else {
+      const int ft = gemm_ft(p.N), ksteps = p.Kd / 32;
+      const int n_tiles = (p.N + ft * 16 - 1) / (ft * 16);
+      p.ksplit = EPI == EPI_PARTS ? gemm_parts_split(n_tiles, ksteps) : gemm_ksplit(n_tiles, ksteps);
+      p.kps = (ksteps + p.ksplit - 1) / p.ksplit;
+      int ksw = (p.kps + MAX_NW - 1) / MAX_NW;
+      ksw = (ksw + 3) / 4 * 4;
+      return launch_tiled<EPI>(p, ksw, st);
+    }
+  }
+  const int NT = (p.M + 15) / 16;
   // 16 features per workgroup unless that makes more than ~8 workgroups per CU (the LM head)
   if (gemm_ft(p.N) == 1) {
     switch (NT) {
