@@ -252,15 +252,16 @@ def copy_calibration(dev, reps=3):
     torch.cuda.synchronize()
 
 
-def traffic_from_profile():
-    """HBM bytes per draft-attention call from the committed counter summary (two rocprofv3 --pmc passes,
-    FETCH_SIZE then WRITE_SIZE, scaled by the copy calibration), or None when it is absent."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "attn_draft_bs1_8k_counters.md")
+def from_profile(name, key, cast=float):
+    """A figure of a committed profile summary (profiles/<name>: lines `key: value`, written from rocprofv3 --pmc
+    passes: HBM traffic per call from FETCH_SIZE / WRITE_SIZE scaled by the copy calibration, MFMA utilisation), or
+    None when it is absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_call:"):
-                    return int(line.split(":")[1])
+                if line.startswith(key + ":"):
+                    return cast(line.split(":")[1])
     except OSError:
         pass
     return None
@@ -610,7 +611,9 @@ def main():
         "prefill_s": round(prefill_s, 2),
         "roofline": {"bound": "hbm", "kernel": "gss_draft_attn (block-diffusion draft attention)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": from_profile("attn_draft_bs1_8k.md", "traffic_bytes_per_call", int),
+                     "mfma_util_pct_counter": from_profile("attn_draft_bs1_8k.md", "mfma_util_pct"),
                      "algorithmic_bytes": ab, "avg_us": round(d_us, 2), "L": L, "W": Kw,
                      "mfma_tflops": round(tflops, 1), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "verify_avg_us": round(v_us, 2)},
@@ -619,6 +622,8 @@ def main():
                              "achieved": round(b_bytes / (b_us * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(b_bytes / (b_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                              "algorithmic_bytes": b_bytes, "avg_us": round(b_us, 2),
+                             "traffic": from_profile("attn_draft_batched32.md", "traffic_bytes_per_call", int),
+                             "mfma_util_pct_counter": from_profile("attn_draft_batched32.md", "mfma_util_pct"),
                              "mfma_tflops": round(b_flops / (b_us * 1e-6) / 1e12, 1),
                              "mfma_frac": round(b_flops / (b_us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                              "by_block_size": by_block},
