@@ -652,10 +652,12 @@ int gemm_parts_split(int n_tiles, int ksteps) {
   return ksteps / ks >= 4 ? ks : 1;
 }
 
+// The partials serve the skinny kernel (M <= 64); the tiled kernel folds its splits in registers, so a workspace
+// sized for 64 rows serves every larger M.
 size_t gemm_ws_bytes(int M, int N, int Kd) {
   const int ft = gemm_ft(N), n_tiles = (N + ft * 16 - 1) / (ft * 16);
   const int ks = gemm_ksplit(n_tiles, Kd / 32);
-  return CTR_BYTES + (ks > 1 ? static_cast<size_t>(ks) * M * N * sizeof(float) : 0);
+  return CTR_BYTES + (ks > 1 ? static_cast<size_t>(ks) * min(M, 64) * N * sizeof(float) : 0);
 }
 
 // ---- batched windows (M > 64): a tiled kernel with gemm_kernel's arithmetic ---------------------------------------

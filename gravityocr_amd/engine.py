@@ -2,8 +2,8 @@
 with every round-to-round quantity (committed lengths, boundary tokens, accept lengths) resident on the device so a
 whole round is captured once as a HIP graph and replayed.
 
-Per layer of a window forward (rows = bs * W, any count: the GEMMs run rows beyond 64 in 64-row slabs with the same
-arithmetic, so every row is computed the same way at every batch size):
+Per layer of a window forward (rows = bs * W, any count: above 64 rows the GEMMs run a tiled kernel with the skinny
+kernel's exact operation sequence, so every row is computed the same way at every batch size):
     gss_gemm_rope_stage             fused q|k|v projection, RoPE on q and k, window K/V staged (not yet in the cache)
     gss_draft_attn / gss_verify_attn   paged prefix + window, draft or verify mask, under the decoder's attention plan
     gss_gemm_parts (o_proj)         fp32 k-split partial sums
@@ -12,7 +12,8 @@ arithmetic, so every row is computed the same way at every batch size):
     gss_gemm_swiglu                 gate_up projection with the SwiGLU epilogue
     gss_gemm_parts (down)           fp32 k-split partial sums
     gss_add_rmsnorm_parts           residual + post-MLP norm + the next layer's input norm
-The prefill (one long prompt) runs its GEMMs through torch.mm; every decode forward runs on the kernels above.
+The prefill (one long prompt) runs the same GEMMs (gss_gemm, gss_gemm_swiglu), gss_rope_stage, gss_kv_commit and
+the verify attention over causal chunks of the prompt.
 A round (the serving full-draft round, patches/sglang/.../selfspec_diffusion_worker.py:660-961):
     draft forward [x0 | MASK x B] -> gss_argmax_accept (argmax only) -> gss_kv_commit of row 0 (x0)
     verify forward [a0, d_1..d_B] -> gss_argmax_accept (argmax + accept + bonus) -> gss_kv_commit of acc+1 rows
@@ -114,8 +115,9 @@ class GssEngine:
         rows = max_bs * max_win
         shapes = [(cfg.qkv_dim, cfg.hidden), (cfg.hidden, cfg.n_heads * cfg.head_dim), (2 * cfg.ffn, cfg.hidden),
                   (cfg.hidden, cfg.ffn), (cfg.vocab, cfg.hidden)]
-        self.ws_gemm = torch.zeros(max(K.gemm_workspace_bytes(rows, n, kd) for n, kd in shapes), dtype=torch.uint8,
-                                   device=dev)
+        # sized at 64 rows or more: every call (the prefill's too) then fits; larger M needs no more
+        self.ws_gemm = torch.zeros(max(K.gemm_workspace_bytes(max(rows, 64), n, kd) for n, kd in shapes),
+                                   dtype=torch.uint8, device=dev)
         self._bufs: Dict[Tuple[int, int], _Bufs] = {}
         self._retired_ws: List[torch.Tensor] = []
 
@@ -253,13 +255,6 @@ class GssEngine:
                pro=dict(a=b.a, h_in=h_a, h_out=None, w_post=self.n_pm[c.n_layers - 1], w_next=self.n_final, eps=eps))
         return b.logits.view(bs, W, c.vocab)
 
-    @staticmethod
-    def _swiglu_torch(x, wgu_il, gu, act):
-        """hipBLASLt gate_up on the interleaved weight, then up * silu(gate) with torch's bf16 rounding."""
-        torch.mm(x, wgu_il.t(), out=gu)
-        g = gu.view(gu.shape[0], -1, 2)
-        torch.mul(g[..., 1], torch.nn.functional.silu(g[..., 0]), out=act)
-
     def commit(self, b: _Bufs, *, n_rows=None, n_add: int = 0, slots=None, seq_lens=None, page_table=None):
         bs = b.bs
         K.kv_commit(b.k_win, b.v_win, self.k_pages, self.v_pages,
@@ -273,40 +268,55 @@ class GssEngine:
     # ------------------------------------------------------------------------------------------ prefill ---------
     def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 48, pos_delta: Optional[torch.Tensor] = None,
                 positions: Optional[torch.Tensor] = None, logits_rows: Optional[Tuple[int, int]] = None):
-        """Causal prefill of one sequence slot from its prompt embeddings [P, H]: whole-prompt GEMMs, attention in
-        causal chunks of ``chunk`` rows through the verify kernel (prefix from the pages, chunk as the window),
-        K/V committed layer by layer. Row j sits at position j (+ pos_delta), or at the M-RoPE positions
-        ``positions`` int32 [P, 3] (t, h, w) when given. Returns the logits of the last prompt row [V] (bf16), or of
-        rows [r0, r1) as [r1 - r0, V] when ``logits_rows`` = (r0, r1)."""
+        """Causal prefill of one sequence slot from its prompt embeddings [P, H]. The layer runs the decode
+        forward's kernels over all P rows (the tiled GEMM above 64 rows): q|k|v with the RoPE epilogue (or, with
+        M-RoPE ``positions``, the plain GEMM and gss_rope_stage_mrope), o_proj and down as k-split parts with the
+        parts norms, gate_up with the SwiGLU epilogue; attention runs in causal chunks of ``chunk`` rows through the
+        verify kernel (prefix from the pages, chunk as the window) under the bs = 1 plan, and K/V is committed layer
+        by layer. Every GEMM and norm computes a row the same way at any row count and the attention does not depend
+        on where a key comes from, so a prefilled row equals the AR step of the same token bit for bit. Row j sits
+        at position j (+ pos_delta), or at the M-RoPE positions ``positions`` int32 [P, 3] (t, h, w) when given.
+        Returns the logits of the last prompt row [V] (bf16), or of rows [r0, r1) as [r1 - r0, V] when
+        ``logits_rows`` = (r0, r1)."""
         c, dev, bf = self.cfg, self.device, torch.bfloat16
         P = emb.shape[0]
         if P > self.max_len:
             raise ValueError("prompt longer than the engine capacity")
         if positions is not None and tuple(positions.shape) != (P, 3):
             raise ValueError("positions must be [P, 3]")
+        eps = c.rms_eps
         pt = self.page_table[slot:slot + 1]
         h = emb.to(device=dev, dtype=bf).contiguous().clone()
         x = torch.empty_like(h)
-        qkv = torch.empty(P, c.qkv_dim, dtype=bf, device=dev)
         q = torch.empty(1, P, c.n_heads, c.head_dim, dtype=bf, device=dev)
         o = torch.empty_like(q)
         kw = torch.empty(1, 1, P, c.n_kv_heads, c.head_dim, dtype=bf, device=dev)
         vw = torch.empty_like(kw)
-        a = torch.empty(P, c.hidden, dtype=bf, device=dev)
+        act = torch.empty(P, c.ffn, dtype=bf, device=dev)
+        parts_path = self.gemm_parts and (c.hidden // 64) % 4 == 0
+        if parts_path:
+            np_o = K.gemm_parts_count(c.hidden, c.n_heads * c.head_dim)
+            np_d = K.gemm_parts_count(c.hidden, c.ffn)
+            parts = torch.empty(max(np_o, np_d), P, c.hidden, dtype=torch.float32, device=dev)
+        else:
+            a = torch.empty(P, c.hidden, dtype=bf, device=dev)
+        qkv = None if positions is None else torch.empty(P, c.qkv_dim, dtype=bf, device=dev)
+        ws_g = self.ws_gemm
         zero = torch.zeros(1, dtype=torch.int32, device=dev)
         starts = torch.arange(0, P, chunk, dtype=torch.int32, device=dev)
         lens = torch.zeros(1, dtype=torch.int32, device=dev)
         pos3 = None if positions is None else positions.to(device=dev, dtype=torch.int32).contiguous()
         plan = self.attn_plan(1)
         ws = self._attn_ws(1, min(chunk, P), plan)
-        K.rmsnorm(h, self.n_in[0], x, c.rms_eps)
+        K.rmsnorm(h, self.n_in[0], x, eps)
         for l in range(c.n_layers):
-            torch.mm(x, self.wqkv[l].t(), out=qkv)
-            if positions is not None:
+            if positions is None:
+                K.gemm_rope_stage(x, self.wqkv[l], zero, self.inv_freq, q, kw[0], vw[0], rot_dim=c.rot_dim,
+                                  pos_delta=pos_delta, workspace=ws_g)
+            else:
+                K.gemm(x, self.wqkv[l], qkv, workspace=ws_g)
                 K.rope_stage_mrope(qkv, pos3, self.inv_freq, q[0], kw[0, 0], vw[0, 0], sections=c.mrope_section,
                                    rot_dim=c.rot_dim)
-            else:
-                K.rope_stage(qkv, zero, self.inv_freq, q, kw[0], vw[0], pos_delta=pos_delta, rot_dim=c.rot_dim)
             lens.zero_()
             K.kv_commit(kw, vw, self.k_pages[l:l + 1], self.v_pages[l:l + 1], pt, lens, self.ws_commit, n_add=P)
             for i, s0 in enumerate(range(0, P, chunk)):
@@ -314,20 +324,24 @@ class GssEngine:
                 K.window_attention(q[:, s0:s0 + n].contiguous(), self.k_pages[l], self.v_pages[l], pt,
                                    starts[i:i + 1], kw[0, :, s0:s0 + n].contiguous(), vw[0, :, s0:s0 + n].contiguous(),
                                    o[:, s0:s0 + n], n_causal=None, scale=self.scale, plan=plan, workspace=ws)
-            torch.mm(o.view(P, -1), self.wo[l].t(), out=a)
-            K.add_rmsnorm(a, self.n_psa[l], h, self.n_pa[l], x, c.rms_eps)
-            gu = torch.empty(P, 2 * c.ffn, dtype=bf, device=dev)
-            act = torch.empty(P, c.ffn, dtype=bf, device=dev)
-            self._swiglu_torch(x, self.wgu[l], gu, act)
-            del gu
-            torch.mm(act, self.wdown[l].t(), out=a)
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
-            K.add_rmsnorm(a, self.n_pm[l], h, nxt, x, c.rms_eps)
+            if parts_path:
+                K.gemm_parts(o.view(P, -1), self.wo[l], parts[:np_o])
+                K.add_rmsnorm_parts(parts[:np_o], self.n_psa[l], h, self.n_pa[l], x, eps)
+                K.gemm_swiglu(x, self.wgu[l], act, workspace=ws_g)
+                K.gemm_parts(act, self.wdown[l], parts[:np_d])
+                K.add_rmsnorm_parts(parts[:np_d], self.n_pm[l], h, nxt, x, eps)
+            else:
+                K.gemm(o.view(P, -1), self.wo[l], a, workspace=ws_g)
+                K.add_rmsnorm(a, self.n_psa[l], h, self.n_pa[l], x, eps)
+                K.gemm_swiglu(x, self.wgu[l], act, workspace=ws_g)
+                K.gemm(act, self.wdown[l], a, workspace=ws_g)
+                K.add_rmsnorm(a, self.n_pm[l], h, nxt, x, eps)
         self.seq_lens[slot:slot + 1].fill_(P)
-        if logits_rows is not None:
-            r0, r1 = logits_rows
-            return x[r0:r1] @ self.lm_head.t()
-        return (x[P - 1:P] @ self.lm_head.t())[0]
+        r0, r1 = logits_rows if logits_rows is not None else (P - 1, P)
+        logits = torch.empty(r1 - r0, c.vocab, dtype=bf, device=dev)
+        K.gemm(x[r0:r1], self.lm_head, logits, workspace=ws_g)
+        return logits if logits_rows is not None else logits[0]
 
 
 @dataclass

@@ -280,8 +280,9 @@ typedef struct gss_norm_epilogue {
 
 /* Workspace of the three GEMMs: per-column-tile counters at a fixed offset (zero them once after allocation; the
  * kernels leave them at zero) and the split-K partials of shapes whose column tiles alone would leave most CUs idle
- * (the k split depends on N and Kd only, never on M, so results stay batch invariant). One workspace sized for the
- * largest (M, N, Kd) serves every call on a stream. */
+ * (the k split depends on N and Kd only, never on M, so results stay batch invariant). Calls with M > 64 fold their
+ * splits inside the kernel and need the counters block only, so the size stops growing at M = 64. One workspace
+ * sized for the largest (M, N, Kd) serves every call on a stream. */
 int gss_gemm_workspace_size(int M, int N, int Kd, size_t* bytes);
 
 int gss_gemm(const void* x, int64_t ldx, const gss_norm_prologue* pro, const void* w, int64_t ldw, void* y,

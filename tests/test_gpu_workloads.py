@@ -22,6 +22,9 @@ geometric(0.1), so accept lengths vary between sequences and rounds):
     a one-sequence AR decode under the batch's attention plan, bit for bit;
   * every round's committed slots equal the page-table rule for the committed positions, -1 past the accept length.
 The prefix K/V is seeded N(0, 0.8) (the spread of this model's projected K/V) written straight into the pages.
+
+The prefill: a 4096-row prompt prefilled in one call equals, for its last 24 rows, a prefill of the first 4072 followed
+by 24 one-row AR steps, bit for bit (logits and every K/V page).
 """
 import numpy as np
 import pytest
@@ -166,6 +169,46 @@ def test_bs1_rounds_at_8k_prefix(cuda, weights16):
         if int(rec["target"][r]) != int(tgt[r]):
             top = torch.topk(vl[r].float(), 2).values
             assert float(top[0] - top[1]) < TOL, (r, "verify argmax differs without a near tie")
+
+
+# ------------------------------------------------------------------------------------- prefill == AR steps ----
+def test_prefill_rows_equal_ar_steps(cuda, weights16):
+    """The prefill runs the decode forward's kernels over all prompt rows (tiled GEMMs above 64 rows, the parts norms,
+    the RoPE epilogue, chunked verify attention under the bs = 1 plan). A prefill of P = 4096 rows (1024 visual
+    embeddings + 3072 ids) therefore gives, for its last n = 24 rows, the logits of n one-row AR steps over a
+    prefill of the first P - n rows, bit for bit, and the same K/V in every page of every layer."""
+    from gravityocr_amd.engine import GssEngine
+    from gravityocr_amd.model import SYNTH_1536 as cfg, synthetic_prompt
+
+    w = weights16
+    P, n = 4096, 24
+    vis, ids = synthetic_prompt(cfg, 1024, P - 1024, seed=5)
+    emb = torch.cat([vis, w["embed"][ids]], 0)
+    eng = GssEngine(cfg, w, max_bs=1, max_len=P + 64, device=cuda)
+    pages = eng.page_table[0, :P // 16].long()
+    print(f"prefill {P}", flush=True)
+    full = eng.prefill(0, emb, logits_rows=(P - n, P))
+    k_full, v_full = eng.k_pages[:, pages].clone(), eng.v_pages[:, pages].clone()
+    torch.cuda.synchronize()
+
+    eng.k_pages.zero_()
+    eng.v_pages.zero_()
+    print(f"prefill {P - n}, then {n} AR steps", flush=True)
+    eng.prefill(0, emb[:P - n])
+    b = eng.bufs(1, 1)
+    emb_dev = emb.to(device=cuda, dtype=torch.bfloat16)
+    steps = []
+    for j in range(n):
+        lg = eng.forward(b, emb=emb_dev[P - n + j].view(1, -1), n_causal=None)
+        steps.append(lg[0, 0].clone())
+        eng.commit(b, n_add=1)
+    torch.cuda.synchronize()
+    assert int(eng.seq_lens[0]) == P
+    step_logits = torch.stack(steps)
+    diff = (step_logits.float() - full.float()).abs().max().item()
+    assert torch.equal(step_logits, full), f"prefill rows differ from AR steps (max |diff| {diff})"
+    assert torch.equal(eng.k_pages[:, pages], k_full), "K pages differ"
+    assert torch.equal(eng.v_pages[:, pages], v_full), "V pages differ"
 
 
 # ----------------------------------------------------------------------------------- 32 ragged sequences ----
