@@ -14,10 +14,12 @@ NON_CAUSAL mask rows + CAUSAL seed row), a verify forward gss_verify_attn (causa
 is the request's committed length (forward_batch.seq_lens) read from the pages, the window's own K/V from the
 forward's k / v. The commit (GssFastCommit) runs gss_ss_commit: packed rows, seeds, the finish cut of every
 request, seq_lens and the page-granular free list in one launch, then one page-locked readback and one extend +
-check_finished per request.
+check_finished per request; with a draft-ahead callback (selfspec_fast_commit.py:357-440), rounds in which no request
+can finish apply their lengths and frees at the readback and launch the next draft before the bookkeeping.
 """
 from typing import Callable, List, Optional
 
+import numpy as np
 import torch
 
 from . import kernels as gk
@@ -161,6 +163,7 @@ class GssFastCommit:
         self.cut_host = torch.zeros(max_bs + 1, pin_memory=True, **i32)
         self.event = torch.cuda.Event()
         self.n_rounds = 0
+        self.n_ahead = self.n_launched = 0   # draft-ahead: rounds settled before the bookkeeping, drafts launched
 
     def _stage_rules(self, reqs) -> None:
         """Host values of the finish rule for this round's requests, then their copies to the device (queued on
@@ -184,9 +187,43 @@ class GssFastCommit:
             d[:bs].copy_(h[:bs], non_blocking=True)
 
     def commit(self, vi, batch, seeds: torch.Tensor, ahead=None):
-        """Returns (next seeds device [bs], tokens per request, j per request)."""
-        if ahead is not None:
-            raise NotImplementedError("the draft-ahead commit is not built")
+        """Returns (next seeds device [bs], tokens per request, j per request).
+
+        ``ahead`` (draft-ahead serving, None = the plain round): a callable ahead(inc) -> bool that launches the next
+        round's draft. When the readback shows that no request can finish this round (``_none_finish``), every cut
+        is the round's full length, so the lengths and the free pages are final at the readback: they are applied
+        (the frees before the next draft allocates), ahead(inc) runs with inc[i] = the length increment of request
+        i, and the per-request bookkeeping follows while that draft runs on the GPU; a launched draft's K slots
+        count in kv_allocated_len. Any other round settles exactly as the plain one."""
+        st = self._launch(vi, batch, seeds)
+        if ahead is None or not self._none_finish(st):
+            return self._settle(st, batch)
+        bs = st["bs"]
+        inc = [int(c) for c in st["cuts"]]
+        batch.seq_lens_cpu += torch.as_tensor(inc, dtype=batch.seq_lens_cpu.dtype)
+        batch.seq_lens_sum += sum(inc)
+        self._free(batch, [self.free_dev[:st["n_free"]]] if st["n_free"] else [])
+        launched = bool(ahead(inc))
+        toks, js = [], []
+        for i, req in enumerate(batch.reqs):
+            T, j = st["T"][i], inc[i]
+            req.output_ids.extend(T)
+            req.check_finished(len(T))
+            if req.finished():
+                raise RuntimeError(f"draft-ahead commit: request {i} finished in a round the readback showed it "
+                                   f"could not finish in (tokens {T})")
+            self._count(req, j, st["acc"][i])
+            req.kv_committed_len += j + 1
+            req.kv_allocated_len = _round_up(req.kv_committed_len + (self.K if launched else 0), self.page)
+            toks.append(T)
+            js.append(j)
+        self.n_rounds += 1
+        self.n_ahead += 1
+        self.n_launched += launched
+        return st["out"], toks, js
+
+    def _launch(self, vi, batch, seeds) -> dict:
+        """The commit kernel and the round's one readback; returns the host view of the round."""
         reqs = batch.reqs
         bs, K, pg = batch.batch_size(), self.K, self.page
         if vi.draft_token_num != K or bs > self.max_bs:
@@ -204,17 +241,51 @@ class GssFastCommit:
         self.event.record()
         self.event.synchronize()                          # the round's one readback
         rows = self.packed_host[:bs].numpy()
-        cuts = self.cut_host[:bs].numpy().tolist()
-        n_free = int(self.cut_host[bs])
-        alloc = batch.token_to_kv_pool_allocator
-        by_rule = self.budget_host[:bs].numpy() >= 0
+        acc = [int(rows[i, 1]) for i in range(bs)]
+        # host lists: the page-locked buffers are rewritten by the next round's copies
+        T = [[int(rows[i, 0])] + rows[i, 2:3 + acc[i]].tolist() for i in range(bs)]
+        return dict(bs=bs, S=S, loc=loc, out=out, acc=acc, T=T, cuts=self.cut_host[:bs].numpy().tolist(),
+                    n_free=int(self.cut_host[bs]), by_rule=(self.budget_host[:bs].numpy() >= 0).tolist())
+
+    def _none_finish(self, st) -> bool:
+        """True when no request of the round can finish: every request is under the cut rule, its remaining budget
+        exceeds the round's token count (so length cannot fire), and none of the round's ids is one of its stop ids
+        or outside [0, vocab]. Then its cut is the last token and check_finished leaves it running."""
+        bs = st["bs"]
+        budget, vocab, stop = (t[:bs].numpy() for t in (self.budget_host, self.vocab_host, self.stop_host))
+        for i in range(bs):
+            T = st["T"][i]
+            if not st["by_rule"][i] or budget[i] <= len(T) or min(T) < 0 or max(T) > vocab[i]:
+                return False
+            ids = stop[i]
+            if np.isin(T, ids[ids >= 0]).any():
+                return False
+        return True
+
+    def _count(self, req, j, a):
+        """acceptance counters: the verified count, or 0 when a0 itself ended the request"""
+        verified = 0 if (j == 0 and req.finished()) else a + 1
+        req.spec_verify_ct += 1
+        req.spec_accepted_tokens += verified
+        req.update_spec_acceptance_histogram(verified)
+
+    @staticmethod
+    def _free(batch, freed):
+        if freed:
+            fl = torch.cat(freed) if len(freed) > 1 else freed[0]
+            # inside a free group the allocator keeps the tensor itself: never hand it a view of a reused buffer
+            alloc = batch.token_to_kv_pool_allocator
+            alloc.free(fl if getattr(alloc, "is_not_in_free_group", True) else fl.clone())
+
+    def _settle(self, st, batch):
+        """Per request: extend + check_finished (or the per-token path), counters, kv lengths; then the host and
+        device lengths and the frees."""
+        K, pg, S, loc = self.K, self.page, st["S"], st["loc"]
         extra_free = []
         toks, js = [], []
-        for i, req in enumerate(reqs):
-            a = int(rows[i, 1])
-            T = [int(rows[i, 0])] + rows[i, 2:3 + a].tolist()
-            j = cuts[i]
-            if by_rule[i]:
+        for i, req in enumerate(batch.reqs):
+            a, T, j = st["acc"][i], st["T"][i], st["cuts"][i]
+            if st["by_rule"][i]:
                 req.output_ids.extend(T[: j + 1])
                 req.check_finished(j + 1)
             else:
@@ -231,22 +302,13 @@ class GssFastCommit:
                     if hi > lo:
                         extra_free.append(loc[i * K + lo:i * K + hi])
                     j = jl
-            # acceptance counters: the verified count, or 0 when a0 itself ended the request
-            verified = 0 if (j == 0 and req.finished()) else a + 1
-            req.spec_verify_ct += 1
-            req.spec_accepted_tokens += verified
-            req.update_spec_acceptance_histogram(verified)
+            self._count(req, j, a)
             req.kv_committed_len += j + 1
             req.kv_allocated_len = _round_up(req.kv_committed_len, pg)
             toks.append(T[: j + 1])
             js.append(j)
         batch.seq_lens_cpu += torch.as_tensor(js, dtype=batch.seq_lens_cpu.dtype)
         batch.seq_lens_sum += sum(js)
-        freed = [self.free_dev[:n_free]] if n_free else []
-        freed += extra_free
-        if freed:
-            fl = torch.cat(freed) if len(freed) > 1 else freed[0]
-            # inside a free group the allocator keeps the tensor itself: never hand it a view of a reused buffer
-            alloc.free(fl if getattr(alloc, "is_not_in_free_group", True) else fl.clone())
+        self._free(batch, ([self.free_dev[:st["n_free"]]] if st["n_free"] else []) + extra_free)
         self.n_rounds += 1
-        return out, toks, js
+        return st["out"], toks, js

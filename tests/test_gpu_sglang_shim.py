@@ -4,7 +4,9 @@
     through req_to_token's page-aligned slots) plus the window, within the attention tolerance (1e-2 * max |ref|);
   * commit equals the oracle's _ss_commit restatement and per-token host loop: next seeds, committed tokens and j,
     seq_lens (device and host), and, at page size 16, the freed pages: exactly the pages of the verify slots that hold
-    no kept token (a page-granular allocator would otherwise release committed KV)."""
+    no kept token (a page-granular allocator would otherwise release committed KV);
+  * the draft-ahead commit settles as the plain one, and calls the next draft's launch before the bookkeeping
+    exactly in the rounds where no request can finish."""
 import numpy as np
 import pytest
 import torch
@@ -156,6 +158,79 @@ def test_fast_commit_pages_and_finish_rules(cuda, bs, finish):
         assert not kept & set(alloc.freed_pages)
     assert sorted(alloc.freed_pages) == sorted(want_pages)
     assert alloc.calls <= 1
+
+
+def _ahead_round(cuda, case, bs, seed):
+    """One commit round's inputs at page size 16 (K = 17): case "clean" draws ids that are neither stop ids (3, 7)
+    nor outside the vocabulary (10) and budgets beyond the round, so no request finishes; "finish" plants stop id 7
+    as request 1's first accepted token; "slow" gives request 2 stop strings (outside the cut rule)."""
+    g = np.random.default_rng(seed)
+    K, vocab, pool_n, page = 17, 10, bs + 4, 16
+    ok = np.array([0, 1, 2, 4, 5, 6, 8, 9])
+    acc = g.integers(0, K, bs).astype(np.int32)
+    predict = ok[g.integers(0, len(ok), bs * K + 1)].astype(np.int32)
+    a0 = ok[g.integers(0, len(ok), bs)].astype(np.int64)
+    if case == "finish":
+        predict[1 * K] = 7
+    rpi = g.permutation(pool_n)[:bs].astype(np.int64)
+    seeds = g.integers(0, 100, pool_n).astype(np.int64)
+    S = g.integers(10, 200, bs).astype(np.int64)
+    pts = [g.permutation(64) + 64 * i for i in range(bs)]
+    loc = np.array([pts[i][(S[i] + r) // page] * page + (S[i] + r) % page for i in range(bs) for r in range(K)],
+                   dtype=np.int64)
+    reqs = [_Req(int(b), vocab) for b in g.integers(K + 2, 100, bs)]
+    for i, r in enumerate(reqs):
+        r.kv_committed_len, r.kv_allocated_len = int(S[i]), int(S[i])
+        if case == "slow" and i == 2:
+            r.sampling_params.stop_strs = ["</s>"]
+    dev = lambda a: torch.as_tensor(a).to(cuda)
+    vi = _NS(predict=dev(predict), accept_length=dev(acc), a0=dev(a0), draft_token_num=K)
+    alloc = _PageAlloc(page)
+    batch = _NS(batch_size=lambda: bs, out_cache_loc=dev(loc), req_pool_indices=dev(rpi), seq_lens=dev(S),
+                seq_lens_cpu=torch.as_tensor(S.copy()), seq_lens_sum=int(S.sum()), reqs=reqs,
+                token_to_kv_pool_allocator=alloc)
+    return vi, batch, dev(seeds), alloc
+
+
+@pytest.mark.parametrize("case,bs", [("clean", 1), ("clean", 4), ("clean", 16), ("finish", 4), ("slow", 4)])
+def test_fast_commit_draft_ahead(cuda, case, bs):
+    """The draft-ahead commit against the plain one on two identical rounds: the same next seeds, seed pool,
+    committed tokens, cuts, device and host lengths, freed pages and counters. ahead(inc) runs exactly when no
+    request finishes in the plain commit and every request is under the cut rule: then once, with inc = the cuts
+    (the length increments), after the frees and before any output_ids is extended, and the launched draft's K
+    slots count in the page-aligned kv_allocated_len. Otherwise the round settles as the plain one."""
+    from gravityocr_amd.sglang_shim import GssFastCommit
+    K, page, seed = 17, 16, 11 * bs + len(case)
+    print(f"draft-ahead commit {case} bs={bs}", flush=True)
+    vi_p, b_p, seeds_p, alloc_p = _ahead_round(cuda, case, bs, seed)
+    vi_a, b_a, seeds_a, alloc_a = _ahead_round(cuda, case, bs, seed)
+    out_p, toks_p, js_p = GssFastCommit(K, 32, cuda, page=page, token_loop=_token_loop).commit(vi_p, b_p, seeds_p)
+    calls = []
+
+    def ahead(inc):
+        calls.append((list(inc), alloc_a.calls, [list(r.output_ids) for r in b_a.reqs]))
+        return True
+
+    fc = GssFastCommit(K, 32, cuda, page=page, token_loop=_token_loop)
+    out_a, toks_a, js_a = fc.commit(vi_a, b_a, seeds_a, ahead=ahead)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_p) and torch.equal(seeds_a, seeds_p)
+    assert toks_a == toks_p and js_a == js_p
+    assert torch.equal(b_a.seq_lens, b_p.seq_lens) and torch.equal(b_a.seq_lens_cpu, b_p.seq_lens_cpu)
+    assert b_a.seq_lens_sum == b_p.seq_lens_sum
+    assert alloc_a.freed_pages == alloc_p.freed_pages and alloc_a.calls == alloc_p.calls
+    none_finish = not any(r.finished() for r in b_p.reqs) and case != "slow"
+    assert none_finish == (case == "clean")
+    assert len(calls) == (1 if none_finish else 0) and fc.n_ahead == fc.n_launched == len(calls)
+    for ra, rp in zip(b_a.reqs, b_p.reqs):
+        assert ra.output_ids == rp.output_ids and ra.finished() == rp.finished() and ra.hist == rp.hist
+        assert ra.kv_committed_len == rp.kv_committed_len
+        want = -(-(rp.kv_committed_len + (K if none_finish else 0)) // page) * page
+        assert ra.kv_allocated_len == want
+    if none_finish:
+        inc, n_free_calls, outs = calls[0]
+        assert inc == js_p == [len(t) - 1 for t in toks_p]
+        assert n_free_calls == alloc_p.calls and all(o == [] for o in outs)
 
 
 def test_fast_commit_without_token_loop_raises_for_slow_requests(cuda):
