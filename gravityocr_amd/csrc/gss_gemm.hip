@@ -665,51 +665,94 @@ size_t gemm_ws_bytes(int M, int N, int Kd) {
 // P_v = the MFMA chain (v_mfma_f32_16x16x32_bf16, weights as A, activations as B, accumulating from zero) over the
 // k-steps [ks*kps + v*ksw, ks*kps + (v+1)*ksw) clipped to the split; the splits are then written as parts or
 // folded in split order. This kernel computes exactly that sequence of operations per element, but with a GEMM
-// tiling: a workgroup owns a BF-feature x BM-row block, its 4 waves a WF x WN grid of 16x16 tiles each, and every
-// wave walks all k-steps of the split itself, restarting its accumulator P at each wave-range boundary (ksw k-steps,
-// a multiple of the 4-k-step LDS chunk) and folding it into S. Weights and activations stream through two LDS
-// buffers of 4 k-steps (direct-to-LDS loads, the next chunk in flight while the current one is computed), rows
-// XOR-swizzled by 16-byte chunk so the 16 rows of a fragment read hit distinct banks. Every weight byte is read
-// once per row block instead of once per 64 rows, and every activation byte once per feature block.
-constexpr int TK = 4;    // k-steps per LDS chunk
-constexpr int TCH = 16;  // 16-byte chunks per LDS row (TK * 32 bf16)
-
+// tiling: a workgroup owns a BF-feature x BM-row block, its GF x GM waves a WF x WN grid of 16x16 tiles each, and
+// every wave walks all k-steps of the split itself, restarting its accumulator P at each wave-range boundary (ksw
+// k-steps, a multiple of the LDS chunk) and folding it into S. Weights and activations stream through a ring of NB
+// LDS buffers of TKC k-steps each (direct-to-LDS loads from a scalar base plus precomputed per-lane offsets, issued
+// NB - 1 chunks ahead; a wave waits only for its loads of the chunk it is about to read, the later chunks stay in
+// flight), rows XOR-swizzled by 16-byte chunk so the 16 rows of a fragment read hit distinct banks; the next k-step's
+// fragments are read while the current one's MFMAs run. Every weight byte is read once per row block instead of once
+// per 64 rows, and every activation byte once per feature block.
 GSS_DEV void dma16_lds(const void* g, const void* lds) {
   const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
 }
 
-template <int EPI, int WF, int WN>
-__global__ void __launch_bounds__(256) gemm_tiled_kernel(GemmParams p, int ksw) {
-  constexpr int BF = 2 * WF * 16, BM = 2 * WN * 16, ROWS = BF + BM;
-  constexpr int PER_WAVE = ROWS * TCH / 64 / 4;  // direct-to-LDS instructions per wave per chunk
-  extern __shared__ __attribute__((aligned(16))) u32x4_t tl[];  // [2][ROWS][TCH]
+// the same load from a wave-uniform base (in SGPRs) plus a 32-bit per-lane byte offset: no 64-bit address math per lane
+GSS_DEV void dma16_lds_s(const void* sbase, uint32_t voff, const void* lds) {
+  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(la) : "memory");
+}
+
+// s_waitcnt on the vector-memory counter alone (at most N of this wave's loads still in flight)
+template <int N>
+GSS_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int EPI, int GF, int GM, int WF, int WN, int TKC, int NB, bool MULTI>
+__global__ void __launch_bounds__(64 * GF * GM) gemm_tiled_kernel(GemmParams p, int ksw) {
+  static_assert(4 % TKC == 0 && NB >= 2 && NB <= 4, "chunks divide the 4-k-step wave-range unit; ring of 2..4");
+  constexpr int NW = GF * GM;                    // waves: GF along the features x GM along the rows
+  constexpr int BF = GF * WF * 16, BM = GM * WN * 16, ROWS = BF + BM;
+  constexpr int CH = TKC * 4;                   // 16-byte chunks per LDS row
+  constexpr int PER_WAVE = ROWS * CH / 64 / NW;  // direct-to-LDS instructions per wave per chunk
+  static_assert(ROWS * CH % (64 * NW) == 0 && BF * CH % (64 * NW) == 0, "whole instructions, weight rows first");
+  extern __shared__ __attribute__((aligned(16))) u32x4_t tl[];  // [NB][ROWS][CH]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wf = wv & 1, wn = wv >> 1;
+  const int wf = wv % GF, wn = wv / GF;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int fb = blockIdx.x * BF, rb = blockIdx.y * BM;
   const int ksteps = p.Kd / 32;
   // splits this workgroup computes: one (EPI_PARTS: blockIdx.z) or all of them, folded in split order
   const int ks_lo = EPI == EPI_PARTS ? static_cast<int>(blockIdx.z) : 0;
   const int ks_hi = EPI == EPI_PARTS ? ks_lo + 1 : p.ksplit;
-  // chunk list: split by split, TK k-steps each from the split's first k-step (the last chunk of a split may be
-  // shorter); wave-range boundaries fall on chunk starts because ksw is a multiple of TK
+  // chunk list: split by split, TKC k-steps each from the split's first k-step (the last chunk of a split may be
+  // shorter); wave-range boundaries fall on chunk starts because ksw is a multiple of TKC
   auto split_beg = [&](int ks) { return ks * p.kps; };
   auto split_end = [&](int ks) { return min(ksteps, (ks + 1) * p.kps); };
   int n_chunks = 0;
-  for (int ks = ks_lo; ks < ks_hi; ++ks) n_chunks += (max(0, split_end(ks) - split_beg(ks)) + TK - 1) / TK;
+  for (int ks = ks_lo; ks < ks_hi; ++ks) n_chunks += (max(0, split_end(ks) - split_beg(ks)) + TKC - 1) / TKC;
+  // a chunk cursor (split, first k-step): past the end of a split it moves to the next split's first k-step
+  auto settle = [&](int& kq, int& sq) {
+    while (kq < ks_hi && sq >= split_end(kq)) {
+      ++kq;
+      if (kq < ks_hi) sq = split_beg(kq);
+    }
+  };
 
-  // chunk i -> (split, first k-step, k-steps): walked in order, so keep a cursor
+  // per-lane byte offsets of a chunk's loads from the matrix base at the chunk's first k-step (row * ld + the lane's
+  // 16 bytes of the row's TKC k-steps); instruction j < JW loads weight rows, the rest activation rows. Rows past
+  // N or M repeat the last one (their results are never stored).
+  constexpr int JW = BF * CH / (64 * NW);
+  uint32_t off[PER_WAVE];
+#pragma unroll
+  for (int j = 0; j < PER_WAVE; ++j) {
+    const int slot = (j * NW + wv) * 64 + lane;  // slot of this lane's 16 bytes in the chunk's LDS image
+    const int r = slot / CH, cp = slot % CH;    // LDS row, physical chunk
+    const int c = cp ^ (r & (CH - 1));          // the logical chunk stored there: k-step c / 4, 8 elements c % 4
+    const int64_t row = j < JW ? min(fb + r, p.N - 1) : min(rb + r - BF, p.M - 1);
+    off[j] = static_cast<uint32_t>(row * (j < JW ? p.ldw : p.ldx) * 2 + (c / 4) * 64 + (c % 4) * 16);
+  }
   auto issue = [&](int ks, int s0, int buf) {
     const int kend = split_end(ks);
-    u32x4_t* base = tl + buf * ROWS * TCH;
+    u32x4_t* base = tl + buf * ROWS * CH;
+    if (s0 + TKC <= kend) {  // a full chunk: scalar base + the per-lane offsets
+      const char* bw = reinterpret_cast<const char*>(p.w) + s0 * 64;
+      const char* bx = reinterpret_cast<const char*>(p.x) + s0 * 64;
+#pragma unroll
+      for (int j = 0; j < PER_WAVE; ++j) dma16_lds_s(j < JW ? bw : bx, off[j], base + (j * NW + wv) * 64);
+      return;
+    }
+    // the last, shorter chunk of a split: k-steps past the split repeat its last one (never used)
 #pragma unroll
     for (int j = 0; j < PER_WAVE; ++j) {
-      const int slot = (j * 4 + wv) * 64 + lane;  // slot of this lane's 16 bytes in the chunk's LDS image
-      const int r = slot / TCH, cp = slot % TCH;  // LDS row, physical chunk
-      const int c = cp ^ (r & 15);                // the logical chunk stored there
-      const int s = min(s0 + c / 4, kend - 1);    // its k-step (past the split: a repeat, never used)
+      const int slot = (j * NW + wv) * 64 + lane;
+      const int r = slot / CH, cp = slot % CH;
+      const int c = cp ^ (r & (CH - 1));
+      const int s = min(s0 + c / 4, kend - 1);
       const uint16_t* src;
       if (r < BF) {
         const int f = min(fb + r, p.N - 1);
@@ -718,84 +761,104 @@ __global__ void __launch_bounds__(256) gemm_tiled_kernel(GemmParams p, int ksw) 
         const int m = min(rb + r - BF, p.M - 1);
         src = p.x + static_cast<int64_t>(m) * p.ldx + s * 32 + (c % 4) * 8;
       }
-      dma16_lds(src, base + (j * 4 + wv) * 64);
+      dma16_lds(src, base + (j * NW + wv) * 64);
     }
   };
 
+  // P: the running range's MFMA chain (restarted by an MFMA on a zero C operand at every range start); S: the
+  // split's fold over the ranges; T: the fold over the splits (MULTI only). S and T start at -0.0, so the first
+  // fold S = -0.0 + P_0 is P_0 exactly (also for a zero of either sign) and no fold needs a select.
+  const floatx4_t nz = {-0.f, -0.f, -0.f, -0.f}, z4 = {0.f, 0.f, 0.f, 0.f};
   floatx4_t P[WF][WN], S[WF][WN], T[WF][WN];
-  auto zero = [](floatx4_t(&a)[WF][WN]) {
 #pragma unroll
-    for (int f = 0; f < WF; ++f)
+  for (int f = 0; f < WF; ++f)
 #pragma unroll
-      for (int n = 0; n < WN; ++n) a[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-  };
-  zero(P);
-  zero(S);
-  zero(T);
+    for (int n = 0; n < WN; ++n) {
+      P[f][n] = z4;
+      S[f][n] = nz;
+      if constexpr (MULTI) T[f][n] = nz;
+    }
   const int fr0 = wf * WF * 16 + l16;          // this lane's A row (feature) in the block, tile 0
   const int mr0 = BF + wn * WN * 16 + l16;     // its B row (activation) in the LDS image, tile 0
+  const int sw = l16 & (CH - 1);               // the swizzle of both (rows = l16 mod 16)
 
-  int ks = ks_lo, s0 = split_beg(ks), v_done = 0;  // cursor: split, chunk start, waves folded into S
-  bool s_set = false;
-  // the first chunk
-  {
-    int kq = ks, sq = s0;
-    while (kq < ks_hi && sq >= split_end(kq)) sq = split_beg(++kq);
-    ks = kq;
-    s0 = sq;
-    if (ks < ks_hi) issue(ks, s0, 0);
-  }
-  for (int i = 0; i < n_chunks; ++i) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    const int kend = split_end(ks), nk = min(TK, kend - s0);
-    // the next chunk's position, then its loads into the other buffer (read by every wave two chunks ago)
-    int ks_n = ks, s_n = s0 + TK;
-    if (s_n >= kend) {
-      ks_n = ks + 1;
-      s_n = ks_n < ks_hi ? split_beg(ks_n) : 0;
+  // the ring: chunks 0 .. NB-2 in flight before the loop, then one more per iteration
+  int ki = ks_lo, si = split_beg(ks_lo), issued = 0;
+  settle(ki, si);
+#pragma unroll
+  for (int q = 0; q < NB - 1; ++q)
+    if (issued < n_chunks) {
+      issue(ki, si, issued % NB);
+      ++issued;
+      si += TKC;
+      settle(ki, si);
     }
-    if (i + 1 < n_chunks) issue(ks_n, s_n, (i + 1) & 1);
-    // a wave-range boundary at this chunk's start: fold P into S
-    if (s0 != split_beg(ks) && (s0 - split_beg(ks)) % ksw == 0) {
+  int ks = ks_lo, s0 = split_beg(ks_lo), v_done = 0;  // compute cursor, ranges folded into S
+  settle(ks, s0);
+  for (int i = 0; i < n_chunks; ++i) {
+    // chunk i has landed once at most (issued - 1 - i) later chunks of this wave are in flight
+    switch (issued - 1 - i) {
+      case 0: wait_vm<0>(); break;
+      case 1: wait_vm<(NB > 2 ? PER_WAVE : 0)>(); break;
+      default: wait_vm<(NB > 3 ? 2 * PER_WAVE : 0)>(); break;
+    }
+    __syncthreads();  // every wave's loads of chunk i landed; every wave is done reading chunk i - 1's buffer
+    if (issued < n_chunks) {  // into the buffer chunk i - 1 used
+      issue(ki, si, issued % NB);
+      ++issued;
+      si += TKC;
+      settle(ki, si);
+    }
+    const int kb = split_beg(ks), kend = split_end(ks), nk = min(TKC, kend - s0);
+    // a range starts at this chunk (ksw is a multiple of TKC): fold the finished one (none at the split's start)
+    const bool restart = (s0 - kb) % ksw == 0;
+    if (restart && s0 != kb) {
 #pragma unroll
       for (int f = 0; f < WF; ++f)
 #pragma unroll
-        for (int n = 0; n < WN; ++n) {
-          S[f][n] = s_set ? S[f][n] + P[f][n] : P[f][n];
-          P[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-        }
-      s_set = true;
+        for (int n = 0; n < WN; ++n) S[f][n] = S[f][n] + P[f][n];
       ++v_done;
     }
-    const u32x4_t* buf = tl + (i & 1) * ROWS * TCH;
+    const u32x4_t* buf = tl + (i % NB) * ROWS * CH;
+    bf16x8_t a[2][WF], b[2][WN];  // fragments of k-step u in set u & 1; k-step u + 1 is read during u's MFMAs
+    auto read = [&](int u, bf16x8_t(&af)[WF], bf16x8_t(&bf)[WN]) {
 #pragma unroll
-    for (int u = 0; u < TK; ++u) {
+      for (int f = 0; f < WF; ++f)
+        af[f] = __builtin_bit_cast(bf16x8_t, buf[(fr0 + f * 16) * CH + ((u * 4 + g4) ^ sw)]);
+#pragma unroll
+      for (int n = 0; n < WN; ++n)
+        bf[n] = __builtin_bit_cast(bf16x8_t, buf[(mr0 + n * 16) * CH + ((u * 4 + g4) ^ sw)]);
+    };
+    read(0, a[0], b[0]);
+#pragma unroll
+    for (int u = 0; u < TKC; ++u) {
       if (u < nk) {  // workgroup-uniform
-        bf16x8_t a[WF], b[WN];
+        if (u + 1 < nk) read(u + 1, a[(u + 1) & 1], b[(u + 1) & 1]);
+        if (u == 0 && restart) {
 #pragma unroll
-        for (int f = 0; f < WF; ++f)
-          a[f] = __builtin_bit_cast(bf16x8_t, buf[(fr0 + f * 16) * TCH + ((u * 4 + g4) ^ l16)]);
+          for (int f = 0; f < WF; ++f)
 #pragma unroll
-        for (int n = 0; n < WN; ++n)
-          b[n] = __builtin_bit_cast(bf16x8_t, buf[(mr0 + n * 16) * TCH + ((u * 4 + g4) ^ l16)]);
+            for (int n = 0; n < WN; ++n)
+              P[f][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0][f], b[0][n], z4, 0, 0, 0);
+        } else {
 #pragma unroll
-        for (int f = 0; f < WF; ++f)
+          for (int f = 0; f < WF; ++f)
 #pragma unroll
-          for (int n = 0; n < WN; ++n) P[f][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[f], b[n], P[f][n], 0, 0, 0);
+            for (int n = 0; n < WN; ++n)
+              P[f][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[u & 1][f], b[u & 1][n], P[f][n], 0, 0, 0);
+        }
       }
     }
-    if (s0 + TK >= kend) {
-      // the split's last chunk: fold the last wave range, then the empty ones of gemm_kernel's last split (+0.0
-      // each: only the sign of a zero can change), then the split's sum
+    if (s0 + TKC >= kend) {
+      // the split's last chunk: fold the last range, then the empty ones of gemm_kernel's last split (+0.0 each:
+      // only the sign of a zero can change), then the split's sum
       const int nw = (p.kps + ksw - 1) / ksw;
 #pragma unroll
       for (int f = 0; f < WF; ++f)
 #pragma unroll
         for (int n = 0; n < WN; ++n) {
-          S[f][n] = s_set ? S[f][n] + P[f][n] : P[f][n];
-          if (v_done + 1 < nw) S[f][n] = S[f][n] + floatx4_t{0.f, 0.f, 0.f, 0.f};
-          P[f][n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+          S[f][n] = S[f][n] + P[f][n];
+          if (v_done + 1 < nw) S[f][n] = S[f][n] + z4;
         }
       if constexpr (EPI == EPI_PARTS) {
 #pragma unroll
@@ -807,17 +870,19 @@ __global__ void __launch_bounds__(256) gemm_tiled_kernel(GemmParams p, int ksw) 
               *reinterpret_cast<floatx4_t*>(static_cast<float*>(p.y) +
                                             (static_cast<int64_t>(ks) * p.M + row) * p.ldy + feat) = S[f][n];
           }
-      } else {
+      } else if constexpr (MULTI) {
 #pragma unroll
         for (int f = 0; f < WF; ++f)
 #pragma unroll
-          for (int n = 0; n < WN; ++n) T[f][n] = ks == ks_lo ? S[f][n] : T[f][n] + S[f][n];
+          for (int n = 0; n < WN; ++n) {
+            T[f][n] = T[f][n] + S[f][n];
+            S[f][n] = nz;
+          }
       }
-      s_set = false;
       v_done = 0;
     }
-    ks = ks_n;
-    s0 = s_n;
+    s0 += TKC;
+    settle(ks, s0);
   }
   if constexpr (EPI != EPI_PARTS) {
 #pragma unroll
@@ -826,33 +891,48 @@ __global__ void __launch_bounds__(256) gemm_tiled_kernel(GemmParams p, int ksw) 
       for (int n = 0; n < WN; ++n) {
         const int row = rb + wn * WN * 16 + n * 16 + l16, feat = fb + wf * WF * 16 + f * 16 + g4 * 4;
         if (row < p.M && feat < p.N)
-          gemm_epilogue<EPI, false>(p, fb + wf * WF * 16, rb + wn * WN * 16, f, n, T[f][n], l16, g4);
+          gemm_epilogue<EPI, false>(p, fb + wf * WF * 16, rb + wn * WN * 16, f, n, MULTI ? T[f][n] : S[f][n], l16,
+                                    g4);
       }
   }
 }
 
-template <int EPI, int WF, int WN>
-int launch_tiled_wf(GemmParams& p, int ksw, hipStream_t st) {
-  constexpr int BF = 2 * WF * 16, BM = 2 * WN * 16;
-  constexpr size_t lds = 2ull * (BF + BM) * TCH * sizeof(u32x4_t);
-  constexpr auto kern = gemm_tiled_kernel<EPI, WF, WN>;
+template <int EPI, int GF, int GM, int WF, int WN, int TKC, int NB, bool MULTI>
+int launch_tiled_k(GemmParams& p, int ksw, hipStream_t st) {
+  constexpr int BF = GF * WF * 16, BM = GM * WN * 16;
+  constexpr size_t lds = static_cast<size_t>(NB) * (BF + BM) * TKC * 4 * sizeof(u32x4_t);
+  constexpr auto kern = gemm_tiled_kernel<EPI, GF, GM, WF, WN, TKC, NB, MULTI>;
   if constexpr (lds > 64 * 1024) {
     if (!allow_full_lds<kern>()) return GSS_ERR_LAUNCH;
   }
   const dim3 grid((p.N + BF - 1) / BF, (p.M + BM - 1) / BM, EPI == EPI_PARTS ? p.ksplit : 1);
-  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, p, ksw);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * GF * GM), lds, st, p, ksw);
   return gss_launch_status();
 }
 
-// The tiled kernel for M > 64: 128 x 128 blocks when they make at least ~one workgroup per CU, else 64 x 64 (any
-// tiling computes the same bits; only the speed depends on it). p.ksplit / p.kps / the wave range ksw are gemm_kernel's
+// several splits folded in the kernel (not EPI_PARTS, which writes each split) take the variant with T
+template <int EPI, int GF, int GM, int WF, int WN, int TKC, int NB>
+int launch_tiled_cfg(GemmParams& p, int ksw, hipStream_t st) {
+  if (EPI != EPI_PARTS && p.ksplit > 1) return launch_tiled_k<EPI, GF, GM, WF, WN, TKC, NB, true>(p, ksw, st);
+  return launch_tiled_k<EPI, GF, GM, WF, WN, TKC, NB, false>(p, ksw, st);
+}
+
+// The tiled kernel for M > 64, by how many blocks each tiling makes (any tiling computes the same bits; only the
+// speed depends on it): 256 x 128 blocks of 8 waves (64 x 64 per wave, two waves per SIMD, a 3-deep ring of
+// 2-k-step chunks) when they give every CU a workgroup (not with several splits folded in the kernel: the extra
+// accumulators would spill), else 128 x 128 blocks of 8 waves (32 x 64 per wave), else 64 x 64 blocks of 4 waves
+// (two workgroups per CU). Measured on the decoder's shapes: the 256 x 128 blocks run the 8192-row gate_up
+// (9216 x 1536) at 340 us against 480 us for 128 x 128 blocks of 4 waves; at 544 rows the 8-wave 128 x 128 blocks
+// take 45 us against 57 us (4 waves) and 49 us (64 x 64). p.ksplit / p.kps / the wave range ksw are gemm_kernel's
 // for the same (N, Kd).
 template <int EPI>
 int launch_tiled(GemmParams& p, int ksw, hipStream_t st) {
-  const int64_t big = static_cast<int64_t>((p.N + 127) / 128) * ((p.M + 127) / 128) *
-                      (EPI == EPI_PARTS ? p.ksplit : 1);
-  if (big >= stream_wgs()) return launch_tiled_wf<EPI, 4, 4>(p, ksw, st);
-  return launch_tiled_wf<EPI, 2, 2>(p, ksw, st);
+  const int z = EPI == EPI_PARTS ? p.ksplit : 1;
+  const bool multi = EPI != EPI_PARTS && p.ksplit > 1;
+  auto blocks = [&](int bf, int bm) { return static_cast<int64_t>((p.N + bf - 1) / bf) * ((p.M + bm - 1) / bm) * z; };
+  if (!multi && blocks(256, 128) >= stream_wgs()) return launch_tiled_k<EPI, 4, 2, 4, 4, 2, 3, false>(p, ksw, st);
+  if (blocks(128, 128) >= stream_wgs()) return launch_tiled_cfg<EPI, 4, 2, 2, 4, 4, 2>(p, ksw, st);
+  return launch_tiled_cfg<EPI, 2, 2, 2, 2, 4, 2>(p, ksw, st);
 }
 
 template <int FT, int NT, int EPI, int PRO, bool POST>
@@ -949,6 +1029,10 @@ int launch_epi(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
       p.kps = (ksteps + p.ksplit - 1) / p.ksplit;
       int ksw = (p.kps + MAX_NW - 1) / MAX_NW;
       ksw = (ksw + 3) / 4 * 4;
+      // the kernel addresses rows by 32-bit byte offsets from the matrix bases
+      if ((static_cast<int64_t>(p.N) - 1) * p.ldw * 2 + p.Kd * 2 >= (int64_t{1} << 32) ||
+          (static_cast<int64_t>(p.M) - 1) * p.ldx * 2 + p.Kd * 2 >= (int64_t{1} << 32))
+        return GSS_ERR_UNSUPPORTED;
       return launch_tiled<EPI>(p, ksw, st);
     }
   }
