@@ -291,39 +291,14 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   const int ng = tb_base + (rw < tb_extra ? 1 : 0);
   __builtin_assume(ng >= NGW - 1 && ng <= NGW);  // the host deals NGW or NGW - 1 tiles to every row wave
   const int nt0 = rg * p.TPG + rw * tb_base + min(rw, tb_extra);
-  bf16x8_t qf[NGW][KS];
-#pragma unroll
-  for (int g = 0; g < NGW; ++g) {
-    const int n = (nt0 + g) * 16 + l16;
-    const int nn = n < p.R ? n : 0;  // padding rows read row 0 (in bounds) and are zeroed
-    const uint16_t* qrow = p.q + ((static_cast<int64_t>(b) * W + nn / p.G) * p.Hq + kvh * p.G + nn % p.G) * D;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qf[g][ks] = (g < ng && n < p.R) ? *reinterpret_cast<const bf16x8_t*>(qrow + ks * 32 + g4 * 8) : bf16x8_t{};
-  }
-
-  // ---- the split's page ids -> LDS, once (their loads are in flight with the query loads above). Stage loads then
-  // take their page ids from LDS, so the only vector-memory loads in flight during the stage loop are the K/V stage
-  // loads themselves, and the wait for one stage never waits for another's.
+  // the split's page ids -> LDS, once; issued right after the query loads, so both are in flight together
   int* spages = reinterpret_cast<int*>(reinterpret_cast<char*>(smem) + Lds<D>::BUF_BYTES);
-  for (int i = tid; i < (t_end - t_beg) * (TILE / PAGE); i += blockDim.x) {
-    const int pos = t_beg * TILE + i * PAGE;
-    spages[i] = pos < L ? pt[pos / PAGE] : 0;
-  }
-  // queries pre-scaled by scale * log2(e) (fp32 product rounded to bf16), so the MFMA yields log2-domain scores
-#pragma unroll
-  for (int g = 0; g < NGW; ++g)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const u32x4_t u = __builtin_bit_cast(u32x4_t, qf[g][ks]);
-      u32x4_t r;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        r[e] = cvt_pk_bf16(__uint_as_float(u[e] << 16) * p.scale_log2,
-                           __uint_as_float(u[e] & 0xffff0000u) * p.scale_log2);
-      qf[g][ks] = __builtin_bit_cast(bf16x8_t, r);
+  auto load_pages = [&]() {
+    for (int i = tid; i < (t_end - t_beg) * (TILE / PAGE); i += blockDim.x) {
+      const int pos = t_beg * TILE + i * PAGE;
+      spages[i] = pos < L ? pt[pos / PAGE] : 0;
     }
-  __syncthreads();
+  };
 
   // ---- tile loads, global -> LDS directly (dma16: lane i of an instruction writes the 16 bytes at the
   // instruction's LDS base + 16 i) into a ring of NSLOT one-tile slots, each K [TILE][D] (XOR-swizzled 16-byte
@@ -381,66 +356,112 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
                           blockDim.x);
     return true;
   };
-
-  // ---- online softmax, private to the wave: key lane kl takes key half kl (32 keys, m-tiles 2 kl and 2 kl + 1)
-  // of every tile of the split, for its ng N-tiles. Scores come out of the MFMA in the log2 domain (the queries are
-  // pre-scaled). Each row keeps a reference max m that trails its running max by at most RESCALE_SLACK, and
-  // P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more than the slack (rare
-  // after the first tiles) does the wave take the row maxima (two xor-shuffles over the row's lanes), move the
-  // references and rescale O and l. P^T is packed to bf16 in the lane that scored it, and O^T += V^T P^T over one
-  // K-step of 32 keys.
-  floatx4_t o[NGW][DT];
-  float m_run[NGW], l_run[NGW];
-#pragma unroll
-  for (int g = 0; g < NGW; ++g) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[g][dt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-    m_run[g] = -INFINITY;
-    l_run[g] = 0.f;
-  }
   const int hsw = (l16 >> 3) & 1;  // the V half swap of head dims d with bit 3 set (d = dt*16 + l16)
   const int vrd = ((g4 >> 1) ^ hsw) * 8 + (g4 & 1) * 4;
   const int hh = kl;               // this wave's key half of every tile
-
   const int n_t = t_end - t_beg;
-  // nothing the compiler tracks may be outstanding when the tile loop starts: a load or spill store still pending
-  // at the loop header would make it wait for every vector memory operation inside the loop, the prefetched tiles
-  // included (a real s_waitcnt, which the compiler's wait insertion accounts for)
-  __builtin_amdgcn_s_waitcnt(0);
-  for (int i = 0; i < min(NSLOT - 1, n_t); ++i) issue_tile(i);
-  for (int i = 0; i < n_t; ++i) {
-    wait_tile(min(NSLOT - 2, n_t - 1 - i));  // this wave's loads of tile i
-    __syncthreads();  // every wave's loads of tile i have landed; every wave is done with tile i - 1's slot
-    if (fix_tile(i)) __syncthreads();  // block-uniform condition
-    if (i + NSLOT - 1 < n_t) issue_tile(i + NSLOT - 1);  // into the slot of tile i - 1
-    const int tb = (t_beg + i) * TILE;
-    const uint16_t* tk = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
-    const uint16_t* tv = tk + TILE_EL;
-    // scores, mask, row maxima and reference moves, P^T, then O^T += V^T P^T. LDS fragments are read one step
-    // ahead of the MFMAs that use them.
-    {
-      floatx4_t sacc[NGW][2];
+
+  // The wave's work for its NG N-tiles, NG a compile-time count (NGW or NGW - 1, dealt by the host), so the MFMA
+  // sequence has no per-tile branches. Both instantiations run the same workgroup barriers in the same order.
+  auto body = [&](auto ngc) {
+    constexpr int NG = decltype(ngc)::value;
+    // ---- query fragments (the B operand of S^T = K Q^T), in registers for the whole kernel: N-tiles
+    // nt0 .. nt0 + NG - 1 of the sequence's R = G*W rows. Rows past R have zero queries and are never written.
+    bf16x8_t qf[NG][KS];
 #pragma unroll
-      for (int g = 0; g < NGW; ++g) sacc[g][0] = sacc[g][1] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-      // K-step outer, m-tile inner: consecutive MFMAs go to 2 * ng different accumulators, so a dependent one
-      // (same accumulator, next K-step) is never issued right behind its predecessor
-      auto kfrag = [&](int i2) {  // i2 = ks * 2 + mt over the half's 2 m-tiles
+    for (int g = 0; g < NG; ++g) {
+      const int n = (nt0 + g) * 16 + l16;
+      const int nn = n < p.R ? n : 0;  // padding rows read row 0 (in bounds) and are zeroed
+      const uint16_t* qrow = p.q + ((static_cast<int64_t>(b) * W + nn / p.G) * p.Hq + kvh * p.G + nn % p.G) * D;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qf[g][ks] = n < p.R ? *reinterpret_cast<const bf16x8_t*>(qrow + ks * 32 + g4 * 8) : bf16x8_t{};
+    }
+    load_pages();
+    // queries pre-scaled by scale * log2(e) (fp32 product rounded to bf16), so the MFMA yields log2-domain scores
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const u32x4_t u = __builtin_bit_cast(u32x4_t, qf[g][ks]);
+        u32x4_t r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          r[e] = cvt_pk_bf16(__uint_as_float(u[e] << 16) * p.scale_log2,
+                             __uint_as_float(u[e] & 0xffff0000u) * p.scale_log2);
+        qf[g][ks] = __builtin_bit_cast(bf16x8_t, r);
+      }
+    __syncthreads();
+
+    // ---- online softmax, private to the wave: key lane kl takes key half kl (32 keys, m-tiles 2 kl and 2 kl + 1)
+    // of every tile of the split, for its NG N-tiles. Scores come out of the MFMA in the log2 domain (the queries
+    // are pre-scaled). Each row keeps a reference max m that trails its running max by at most RESCALE_SLACK, and
+    // P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more than the slack
+    // (rare after the first tiles) does the wave take the row maxima (two xor-shuffles over the row's lanes), move
+    // the references and rescale O and l. P^T is packed to bf16 in the lane that scored it, and O^T += V^T P^T over
+    // one K-step of 32 keys.
+    floatx4_t o[NG][DT];
+    float m_run[NG], l_run[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[g][dt] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      m_run[g] = -INFINITY;
+      l_run[g] = 0.f;
+    }
+    // nothing the compiler tracks may be outstanding when the tile loop starts: a load or spill store still pending
+    // at the loop header would make it wait for every vector memory operation inside the loop, the prefetched tiles
+    // included (a real s_waitcnt, which the compiler's wait insertion accounts for)
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int i = 0; i < min(NSLOT - 1, n_t); ++i) issue_tile(i);
+    for (int i = 0; i < n_t; ++i) {
+      wait_tile(min(NSLOT - 2, n_t - 1 - i));  // this wave's loads of tile i
+      __syncthreads();  // every wave's loads of tile i have landed; every wave is done with tile i - 1's slot
+      if (fix_tile(i)) __syncthreads();  // block-uniform condition
+      if (i + NSLOT - 1 < n_t) issue_tile(i + NSLOT - 1);  // into the slot of tile i - 1
+      const int tb = (t_beg + i) * TILE;
+      const uint16_t* tk = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
+      const uint16_t* tv = tk + TILE_EL;
+      // scores: the half's K fragments (2 m-tiles x KS K-steps) are read in two batches, the second in flight
+      // under the first batch's MFMAs; K-step outer and m-tile inner, each accumulator over the K-steps in order
+      floatx4_t sacc[NG][2];
+#pragma unroll
+      for (int g = 0; g < NG; ++g) sacc[g][0] = sacc[g][1] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+      constexpr int KB = KS;  // fragments per batch (i2 = ks * 2 + mt)
+      auto kfrag = [&](int i2) {
         return *reinterpret_cast<const bf16x8_t*>(&tk[k_lds_index<D>((2 * hh + (i2 & 1)) * 16 + l16, (i2 >> 1) * 4 + g4)]);
       };
-      bf16x8_t a_cur = kfrag(0);
+      bf16x8_t kf[2][KB];
 #pragma unroll
-      for (int i2 = 0; i2 < 2 * KS; ++i2) {
-        bf16x8_t a_nxt = a_cur;
-        if (i2 + 1 < 2 * KS) a_nxt = kfrag(i2 + 1);
+      for (int j = 0; j < KB; ++j) kf[0][j] = kfrag(j);
 #pragma unroll
-        for (int g = 0; g < NGW; ++g)
-          if (g < ng)
-            sacc[g][i2 & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_cur, qf[g][i2 >> 1], sacc[g][i2 & 1], 0, 0, 0);
-        a_cur = a_nxt;
+      for (int bt = 0; bt < 2; ++bt) {
+        if (bt == 0) {
+#pragma unroll
+          for (int j = 0; j < KB; ++j) kf[1][j] = kfrag(KB + j);
+        }
+#pragma unroll
+        for (int j = 0; j < KB; ++j) {
+          const int i2 = bt * KB + j;
+#pragma unroll
+          for (int g = 0; g < NG; ++g)
+            sacc[g][i2 & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[bt][j], qf[g][i2 >> 1], sacc[g][i2 & 1], 0, 0, 0);
+        }
       }
+      // the V^T fragments do not depend on the scores: the first half is read now, under the softmax, the rest
+      // under the first half's MFMAs
+      bf16x8_t vf[DT];
+      auto vfrag = [&](int dt) {
+        const int d = dt * 16 + l16;
+        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh) * D + d) * PAGE + vrd]);
+        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh + 1) * D + d) * PAGE + vrd]);
+        return __builtin_bit_cast(bf16x8_t, u32x4_t{v0[0], v0[1], v1[0], v1[1]});
+      };
+#pragma unroll
+      for (int dt = 0; dt < DT / 2; ++dt) vf[dt] = vfrag(dt);
       if (tb + TILE > L) {  // keys past the prefix: the window mask (wave-uniform branch)
 #pragma unroll
-        for (int g = 0; g < NGW; ++g) {
+        for (int g = 0; g < NG; ++g) {
           const int n = (nt0 + g) * 16 + l16;
           const int roww = (n < p.R ? n : 0) / p.G;  // the row's window index
 #pragma unroll
@@ -454,10 +475,9 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
             }
         }
       }
-      bf16x8_t pb[NGW];
+      bf16x8_t pb[NG];
 #pragma unroll
-      for (int g = 0; g < NGW; ++g) {
-        if (g >= ng) continue;  // wave-uniform
+      for (int g = 0; g < NG; ++g) {
         // the lane's own max over its 8 scores of the row; a row's reference moves only when its max exceeds it by
         // more than the slack (or on its first visible keys, m_run = -inf), so the row max over the row's 4 lanes
         // (two xor-shuffles) is needed only when some lane's own max does: the wave votes first. Keys that are all
@@ -490,91 +510,84 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
         l_run[g] += ls;
         pb[g] = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
       }
-      auto vfrag = [&](int dt) {
-        const int d = dt * 16 + l16;
-        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh) * D + d) * PAGE + vrd]);
-        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh + 1) * D + d) * PAGE + vrd]);
-        return __builtin_bit_cast(bf16x8_t, u32x4_t{v0[0], v0[1], v1[0], v1[1]});
-      };
-      bf16x8_t v_cur = vfrag(0);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        bf16x8_t v_nxt = v_cur;
-        if (dt + 1 < DT) v_nxt = vfrag(dt + 1);
+      for (int dt = DT / 2; dt < DT; ++dt) vf[dt] = vfrag(dt);
 #pragma unroll
-        for (int g = 0; g < NGW; ++g)
-          if (g < ng) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(v_cur, pb[g], o[g][dt], 0, 0, 0);
-        v_cur = v_nxt;
-      }
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int g = 0; g < NG; ++g) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt], pb[g], o[g][dt], 0, 0, 0);
     }
-  }
 
-  // ---- combine the KL key lanes of each row wave in lane order (fp32, through LDS), normalize, write.
+    // ---- combine the KL key lanes of each row wave in lane order (fp32, through LDS), normalize, write.
 #pragma unroll
-  for (int g = 0; g < NGW; ++g) {
-    l_run[g] += __shfl_xor(l_run[g], 16, 64);
-    l_run[g] += __shfl_xor(l_run[g], 32, 64);
-  }
-  __syncthreads();  // every wave is done with the stage buffers: reuse them as scratch
-  float* scr = reinterpret_cast<float*>(smem);
-  // slot of (row wave, key lane k >= 1, N-tile g): O^T [DT][64 lanes] x 4, then m [16 rows], l [16 rows]
-  auto slot = [&](int k, int g) {
-    return scr + static_cast<size_t>((rw * (KL - 1) + k - 1) * NGW + g) * Lds<D>::SCR_FLOATS;
+    for (int g = 0; g < NG; ++g) {
+      l_run[g] += __shfl_xor(l_run[g], 16, 64);
+      l_run[g] += __shfl_xor(l_run[g], 32, 64);
+    }
+    __syncthreads();  // every wave is done with the stage buffers: reuse them as scratch
+    float* scr = reinterpret_cast<float*>(smem);
+    // slot of (row wave, key lane k >= 1, N-tile g): O^T [DT][64 lanes] x 4, then m [16 rows], l [16 rows]
+    auto slot = [&](int k, int g) {
+      return scr + static_cast<size_t>((rw * (KL - 1) + k - 1) * NGW + g) * Lds<D>::SCR_FLOATS;
+    };
+    if (kl != 0) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        float* sl = slot(kl, g);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) reinterpret_cast<floatx4_t*>(sl)[dt * 64 + lane] = o[g][dt];
+        if (g4 == 0) {
+          sl[DT * 256 + l16] = m_run[g];
+          sl[DT * 256 + 16 + l16] = l_run[g];
+        }
+      }
+    }
+    __syncthreads();
+    if (kl != 0) return;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      const int n = (nt0 + g) * 16 + l16;
+      float M = m_run[g];
+#pragma unroll
+      for (int k = 1; k < KL; ++k) M = fmaxf(M, slot(k, g)[DT * 256 + l16]);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      const float a0 = fast_exp2(m_run[g] - Mu);
+      float lc = l_run[g] * a0;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * a0;
+#pragma unroll
+      for (int k = 1; k < KL; ++k) {
+        const float* sl = slot(k, g);
+        const float ak = fast_exp2(sl[DT * 256 + l16] - Mu);
+        lc += sl[DT * 256 + 16 + l16] * ak;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[g][dt] += reinterpret_cast<const floatx4_t*>(sl)[dt * 64 + lane] * ak;
+      }
+      if (n >= p.R) continue;
+      const float inv = lc > 0.f ? 1.f / lc : 0.f;
+      uint16_t* orow;
+      if (p.n_split == 1) {
+        orow = p.out + ((static_cast<int64_t>(b) * W + n / p.G) * p.Hq + kvh * p.G + n % p.G) * D;
+      } else {
+        const int64_t rowid = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.R + n;  // (m, l): [bs, Hkv, R, n_split]
+        orow = p.ws_o + ((static_cast<int64_t>(b) * p.Hkv + kvh) * p.n_split + s) * p.R * D +
+               static_cast<int64_t>(n) * D;
+        if (g4 == 0) {
+          p.ws_ml[(rowid * p.n_split + s) * 2 + 0] = M;
+          p.ws_ml[(rowid * p.n_split + s) * 2 + 1] = lc;
+        }
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<u32x2_t*>(orow + dt * 16 + g4 * 4) =
+            u32x2_t{cvt_pk_bf16(o[g][dt][0] * inv, o[g][dt][1] * inv), cvt_pk_bf16(o[g][dt][2] * inv, o[g][dt][3] * inv)};
+    }
   };
-  if (kl != 0) {
-#pragma unroll
-    for (int g = 0; g < NGW; ++g) {
-      if (g >= ng) continue;
-      float* sl = slot(kl, g);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) reinterpret_cast<floatx4_t*>(sl)[dt * 64 + lane] = o[g][dt];
-      if (g4 == 0) {
-        sl[DT * 256 + l16] = m_run[g];
-        sl[DT * 256 + 16 + l16] = l_run[g];
-      }
-    }
-  }
-  __syncthreads();
-  if (kl != 0) return;
-#pragma unroll
-  for (int g = 0; g < NGW; ++g) {
-    if (g >= ng) continue;
-    const int n = (nt0 + g) * 16 + l16;
-    float M = m_run[g];
-#pragma unroll
-    for (int k = 1; k < KL; ++k) M = fmaxf(M, slot(k, g)[DT * 256 + l16]);
-    const float Mu = M == -INFINITY ? 0.f : M;
-    const float a0 = fast_exp2(m_run[g] - Mu);
-    float lc = l_run[g] * a0;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * a0;
-#pragma unroll
-    for (int k = 1; k < KL; ++k) {
-      const float* sl = slot(k, g);
-      const float ak = fast_exp2(sl[DT * 256 + l16] - Mu);
-      lc += sl[DT * 256 + 16 + l16] * ak;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[g][dt] += reinterpret_cast<const floatx4_t*>(sl)[dt * 64 + lane] * ak;
-    }
-    if (n >= p.R) continue;
-    const float inv = lc > 0.f ? 1.f / lc : 0.f;
-    uint16_t* orow;
-    if (p.n_split == 1) {
-      orow = p.out + ((static_cast<int64_t>(b) * W + n / p.G) * p.Hq + kvh * p.G + n % p.G) * D;
-    } else {
-      const int64_t rowid = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.R + n;  // (m, l): [bs, Hkv, R, n_split]
-      orow = p.ws_o + ((static_cast<int64_t>(b) * p.Hkv + kvh) * p.n_split + s) * p.R * D +
-             static_cast<int64_t>(n) * D;
-      if (g4 == 0) {
-        p.ws_ml[(rowid * p.n_split + s) * 2 + 0] = M;
-        p.ws_ml[(rowid * p.n_split + s) * 2 + 1] = lc;
-      }
-    }
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<u32x2_t*>(orow + dt * 16 + g4 * 4) =
-          u32x2_t{cvt_pk_bf16(o[g][dt][0] * inv, o[g][dt][1] * inv), cvt_pk_bf16(o[g][dt][2] * inv, o[g][dt][3] * inv)};
-  }
+  static_assert(NGW >= 2, "row waves take NGW or NGW - 1 >= 1 N-tiles");
+  if (ng == NGW)
+    body(std::integral_constant<int, NGW>{});
+  else
+    body(std::integral_constant<int, NGW - 1>{});
 }
 
 // Row-group kernel for small batches (bs * Hkv below the wide threshold), where the chip must be filled from few
