@@ -30,6 +30,7 @@ SIGNATURES = {
     "gss_kv_meta": ([_p, _i64, _i64, _p, _p, _i, _p, _p, _i64, _i, _p], _i),
     "gss_log_append": ([_p, _i, _p, _p, _i, _p, _p, _i, _p, _p, _i, _p], _i),
     "gss_penalize_rows": ([_p, _i64, _i, _i, _i, _p, _p, _p], _i),
+    "gss_apply_vocab_mask": ([_p, _i64, _i, _i, _p, _i64, _p], _i),
     "gss_sample_workspace_size": ([_i, _i, _psz], _i),
     "gss_sample_rows": ([_p, _i64, _i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p], _i),
     "gss_gemm_workspace_size": ([_i, _i, _i, _psz], _i),

@@ -377,7 +377,32 @@ size_t sv_ws_bytes(int bs, int K) {
   return static_cast<size_t>(bs) * COUNTER_STRIDE * sizeof(uint32_t) + static_cast<size_t>(bs) * K * 2 * sizeof(uint32_t);
 }
 
+// Grammar vocabulary mask: logits[r, v] = -inf where bit v % 32 of word v / 32 of row r's mask is clear. One thread
+// per mask word (32 tokens); rows in blockIdx.y.
+constexpr int MASK_THREADS = 256;
+__global__ void __launch_bounds__(MASK_THREADS) vocab_mask_kernel(float* logits, int64_t ld_row, int V,
+                                                                  const int32_t* mask, int64_t ld_mask) {
+  const int w = blockIdx.x * MASK_THREADS + threadIdx.x, r = blockIdx.y;
+  if (w * 32 >= V) return;
+  const uint32_t bits = static_cast<uint32_t>(mask[r * ld_mask + w]);
+  if (bits == 0xffffffffu) return;
+  float* row = logits + r * ld_row + w * 32;
+  const int n = min(32, V - w * 32);
+  for (int i = 0; i < n; ++i)
+    if (!((bits >> i) & 1u)) row[i] = -INFINITY;
+}
+
 }  // namespace
+
+extern "C" int gss_apply_vocab_mask(float* logits, int64_t ld_row, int rows, int V, const int32_t* mask,
+                                    int64_t ld_mask, gss_stream_t stream) {
+  if (!logits || !mask || rows <= 0 || V <= 0 || ld_row < V || ld_mask < (V + 31) / 32) return GSS_ERR_ARG;
+  if (rows > 65535) return GSS_ERR_UNSUPPORTED;
+  const dim3 grid(((V + 31) / 32 + MASK_THREADS - 1) / MASK_THREADS, rows);
+  hipLaunchKernelGGL(vocab_mask_kernel, grid, dim3(MASK_THREADS), 0, static_cast<hipStream_t>(stream), logits, ld_row,
+                     V, mask, ld_mask);
+  return gss_launch_status();
+}
 
 extern "C" int gss_penalize_rows(float* logits, int64_t ld_row, int bs, int K, int V, const int32_t* cand,
                                  const gss_penalties* pen, gss_stream_t stream) {

@@ -471,6 +471,19 @@ def penalize_rows(logits, cand, state, order):
                                   _stream()), "gss_penalize_rows")
 
 
+def apply_vocab_mask(logits, mask):
+    """In place on fp32 logit rows [rows, V]: -inf where the packed int32 grammar mask [rows, ceil(V/32)] has the
+    token's bit clear (gss_apply_vocab_mask)."""
+    rows, V = logits.shape
+    _need(mask, torch.int32, "mask")
+    if logits.dtype != torch.float32 or logits.stride(1) != 1:
+        raise ValueError("logits must be fp32 rows")
+    if mask.shape[0] != rows or mask.shape[1] < (V + 31) // 32 or mask.stride(1) != 1:
+        raise ValueError("mask shape")
+    check(lib().gss_apply_vocab_mask(_ptr(logits), logits.stride(0), rows, V, _ptr(mask), mask.stride(0), _stream()),
+          "gss_apply_vocab_mask")
+
+
 def sample_workspace_bytes(bs, K) -> int:
     n = ctypes.c_size_t(0)
     check(lib().gss_sample_workspace_size(bs, K, ctypes.byref(n)), "gss_sample_workspace_size")

@@ -10,8 +10,14 @@ state; verify forward on [a0, d_1..d_{K-1}]; every verify row gets AR's penaltie
 Coins are in (0, 1] (a zero-probability draft token is never accepted), uniforms in [0, 1), both from torch's
 device generator, so a round can be captured into a HIP graph.
 
-Not built: grammar vocabulary masks and custom logit processors (host-side objects of the serving stack), and the
-flashinfer backend's min-p path (its top-k / top-p renormalizations are flashinfer's own kernels): they raise.
+Grammar vocabulary masks and custom logit processors are host-side objects of the serving stack: a round that uses
+them (``SamplingSpec.grammar`` / ``custom_logit_processor``) reads a0 and the draft back after the draft forward,
+walks each grammar along [a0, d_1..] to build the verify rows' packed masks (fulldraft_bitmask,
+selfspec_sampling.py:305-337), and processes the rows in the serving order (selfspec_fast_commit.py:170-194):
+penalties, the grammar mask (gss_apply_vocab_mask), logit_bias, then the custom processor once per row position
+with a read-only request view whose output_ids hold that row's prefix (apply_custom_rows, selfspec_sampling.py:
+200-221). Such rounds synchronize with the host twice and are not captured. Not built: the flashinfer backend's
+min-p path (its top-k / top-p renormalizations are flashinfer's own kernels): it raises.
 """
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
@@ -39,16 +45,84 @@ class SamplingSpec:
     stop_token_ids: Sequence[int] = ()
     logit_bias: Optional[torch.Tensor] = None     # [bs, V] fp32
     order: Sequence[str] = ("frequency", "min_new_tokens", "presence", "repetition")
-    grammar: object = None
-    custom_logit_processor: object = None
+    grammar: object = None                 # per-sequence grammar objects (None entries: no grammar) or None
+    custom_logit_processor: object = None  # callable(logits_rows [n, V] fp32, params list) -> logits rows
+    custom_params: Optional[Sequence] = None  # per-sequence params (a dict's "__req__" gets the row's request view)
+
+
+class RequestView:
+    """Read-only stand-in for a request inside a custom logit processor applied to verify row j: output_ids = the
+    request's committed output ids + the tokens row j's prefix adds; every other attribute is the request's own."""
+
+    __slots__ = ("_req", "output_ids")
+
+    def __init__(self, req, extra):
+        object.__setattr__(self, "_req", req)
+        object.__setattr__(self, "output_ids", list(getattr(req, "output_ids", [])) + [int(t) for t in extra])
+
+    def __getattr__(self, name):
+        return getattr(object.__getattribute__(self, "_req"), name)
+
+    def __setattr__(self, name, value):
+        raise AttributeError("RequestView is read-only")
+
+
+def _allowed(mask_row, tok: int) -> bool:
+    return bool((int(mask_row[tok >> 5]) >> (tok & 31)) & 1)
+
+
+def grammar_masks(grammars, cand, V: int, first_accepted: bool = True):
+    """Packed int32 vocabulary masks [bs * K, ceil(V / 32)] (host) of windows cand [bs, K] (host ints): row j of
+    sequence b allows what b's grammar allows after cand[b, 0..j] (with ``first_accepted`` False, after
+    cand[b, 1..j]: row 0 is the grammar's current state). Each grammar accepts the window's tokens while the previous
+    row allows them, fills its rows, and is rolled back to the state it came in; rows of a sequence without a
+    grammar, of a terminated grammar, and past a token its previous row forbids stay all-allowed. Grammar objects
+    follow the serving stack's surface: allocate_vocab_mask, fill_vocab_mask, accept_token, rollback,
+    is_terminated (selfspec_sampling.py:305-337)."""
+    bs, K = len(cand), len(cand[0])
+    first = next(g for g in grammars if g is not None)
+    mask = first.allocate_vocab_mask(vocab_size=V, batch_size=bs * K, device="cpu")
+    mask.fill_(-1)
+    for b, g in enumerate(grammars):
+        if g is None or g.is_terminated():
+            continue
+        n_acc = 0
+        try:
+            if first_accepted:
+                try:
+                    g.accept_token(int(cand[b][0]))
+                    n_acc += 1
+                except ValueError:
+                    continue
+            for j in range(K):
+                g.fill_vocab_mask(mask, b * K + j)
+                if j + 1 >= K or g.is_terminated():
+                    break
+                nxt = int(cand[b][j + 1])
+                if not _allowed(mask[b * K + j], nxt):
+                    break
+                g.accept_token(nxt)
+                n_acc += 1
+        finally:
+            if n_acc:
+                g.rollback(n_acc)
+    return mask
 
 
 class SampledSelfSpec:
     """Sampled rounds (and the matching AR step) over a SelfSpecDecoder's engine, buffers and logs."""
 
     def __init__(self, dec: SelfSpecDecoder, spec: SamplingSpec):
-        if spec.grammar is not None or spec.custom_logit_processor is not None:
-            raise NotImplementedError("grammar masks and custom logit processors are not built")
+        self.grammars = None
+        if spec.grammar is not None:
+            gl = list(spec.grammar)
+            if len(gl) != dec.bs:
+                raise ValueError("one grammar entry per sequence")
+            self.grammars = gl if any(g is not None for g in gl) else None
+        self.custom = spec.custom_logit_processor
+        if self.custom is not None and (spec.custom_params is None or len(spec.custom_params) != dec.bs):
+            raise ValueError("custom_logit_processor needs one custom_params entry per sequence")
+        self.hosted = self.grammars is not None or self.custom is not None
         if spec.filter == "joint" and _any_positive(spec.min_p):
             raise NotImplementedError("min_p with the flashinfer backend (its renorm kernels) is not built; "
                                       "use filter='torch'")
@@ -108,10 +182,35 @@ class SampledSelfSpec:
                        torch.ones(self.dec.bs, 1, dtype=torch.bool, device=self.dec.st.x0.device))
 
     # ---- pieces ----------------------------------------------------------------------------------------------
-    def _process(self, logits, cand):
-        """AR's logits processing of rows [bs*K, V] (in place) for the prefixes cand[b, 0..r]."""
-        if self.processed:
-            K.penalize_rows(logits, cand, {k: v for k, v in self.state.items()}, self.order)
+    def _process(self, logits, cand, mask=None, cand_host=None, extra_from: int = 0):
+        """AR's logits processing of rows [bs*K, V] (in place) for the prefixes cand[b, 0..r]: penalties, then (a
+        hosted round) the grammar mask, logit_bias and the custom processor with the rows' request views (prefix
+        tokens cand_host[b][extra_from..r])."""
+        if not self.hosted:
+            if self.processed:
+                K.penalize_rows(logits, cand, {k: v for k, v in self.state.items()}, self.order)
+            return
+        bias = self.state.get("logit_bias")
+        if self.order:
+            st = {k: v for k, v in self.state.items() if k != "logit_bias"}
+            K.penalize_rows(logits, cand, st, self.order)
+        if mask is not None:
+            K.apply_vocab_mask(logits, mask)
+        Kr = cand.shape[1]
+        if bias is not None:
+            logits.add_(torch.repeat_interleave(bias, Kr, dim=0))
+        if self.custom is not None:
+            users = list(range(self.dec.bs))
+            for j in range(Kr):
+                params = []
+                for b in users:
+                    prm = self.spec.custom_params[b]
+                    if isinstance(prm, dict) and "__req__" in prm:
+                        prm = dict(prm)
+                        prm["__req__"] = RequestView(prm["__req__"], cand_host[b][extra_from:j + 1])
+                    params.append(prm)
+                rows = torch.tensor([b * Kr + j for b in users], device=logits.device, dtype=torch.int64)
+                logits[rows] = self.custom(logits[rows], params)
 
     def _draw(self, logits, bs, Kr, uniforms, out):
         K.sample_rows(logits, bs, Kr, temperature=self.temperature, filter=self.spec.filter, top_k=self.top_k,
@@ -139,6 +238,8 @@ class SampledSelfSpec:
 
     # ---- the round -------------------------------------------------------------------------------------------
     def round(self, keep: bool = False):
+        if self.hosted:
+            return self._round_hosted(keep)
         d, e, s = self.dec, self.dec.eng, self.dec.st
         bs, Kw = d.bs, s.K
         V = e.cfg.vocab
@@ -169,18 +270,77 @@ class SampledSelfSpec:
         self._cumulate(s.tgt, valid)
         K.log_append(s.ctr, [(s.packed, s.log), (s.am, d.log_am), (s.tgt, d.log_tgt)])
 
+    def _round_hosted(self, keep: bool):
+        """The round with grammar masks and / or custom processors: a0's row is processed against the current
+        grammar states, the verify rows against the states after [a0, d_1..d_j]; the committed tokens then advance
+        the grammars."""
+        d, e, s = self.dec, self.dec.eng, self.dec.st
+        bs, Kw = d.bs, s.K
+        V = e.cfg.vocab
+        dev = s.am.device
+        if bs > 1:
+            s.win[:, 0].copy_(s.x0)
+        lg = d._fwd(d.draft_b, s.win, n_causal=1, logits_f32=True)
+        e.argmax(lg, s.am)
+        row0 = lg[:, 0, :]
+        m0 = None
+        if self.grammars is not None:
+            cur = [[0] for _ in range(bs)]
+            m0 = grammar_masks(self.grammars, cur, V, first_accepted=False).to(dev)
+        self._process(row0, self.a0_cand, m0, [[] for _ in range(bs)], 0)
+        self.u_a0.uniform_()
+        self._draw(row0, bs, 1, self.u_a0, self.a0_tok)
+        s.am[:, 0].copy_(self.a0_tok[:, 0])
+        self._cumulate(self.a0_tok, torch.ones_like(self.a0_tok, dtype=torch.bool))
+        d._commit(d.draft_b, n_add=1)
+        cand = s.am.cpu().tolist()                                 # a0, d_1..d_{K-1} (host)
+        mv = None if self.grammars is None else grammar_masks(self.grammars, cand, V).to(dev)
+        lg = d._fwd(d.verify_b, s.am, n_causal=None, logits_f32=True)
+        rows = lg.view(bs * Kw, V)
+        self._process(rows, s.am, mv, cand, 0)
+        self.coins.uniform_().neg_().add_(1.0)
+        self.u.uniform_()
+        if keep:
+            self.keep = (rows.clone(), self.coins.clone(), self.u.clone(), s.am.clone())
+        K.sample_rows(rows, bs, Kw, temperature=self.temperature, filter=self.spec.filter, top_k=self.top_k,
+                      top_p=self.top_p, min_p=self.min_p, cand=s.am, coins=self.coins, uniforms=self.u,
+                      sampled=self.sampled, target=s.tgt, accept_len=s.acc, next_x0=s.x0, packed=s.packed,
+                      workspace=self.ws)
+        d._commit(d.verify_b, n_rows=s.acc, n_add=1, slots=s.slots)
+        valid = torch.arange(Kw, device=s.acc.device)[None, :] <= s.acc[:, None]
+        self._cumulate(s.tgt, valid)
+        K.log_append(s.ctr, [(s.packed, s.log), (s.am, d.log_am), (s.tgt, d.log_tgt)])
+        if self.grammars is not None:                           # the committed tokens: a0, t_0..t_acc
+            packed = s.packed.cpu().tolist()
+            for b, g in enumerate(self.grammars):
+                if g is None:
+                    continue
+                row = packed[b]
+                for t in [row[0]] + row[2:3 + row[1]]:
+                    if g.is_terminated():
+                        break
+                    g.accept_token(int(t))
+
     def ar_step(self):
         """One sampled AR decode step with the same processing (the reference distribution of the round)."""
         d, e = self.dec, self.dec.eng
         lg = d._fwd(d.ar_b, d.ar_ids, n_causal=None, logits_f32=True)
         row = lg[:, 0, :]
-        self._process(row, self.ar_cand)
+        m = None
+        if self.grammars is not None:
+            m = grammar_masks(self.grammars, [[0] for _ in range(d.bs)], e.cfg.vocab, first_accepted=False)
+            m = m.to(row.device)
+        self._process(row, self.ar_cand, m, [[] for _ in range(d.bs)], 0)
         self.ar_u.uniform_()
         self._draw(row, d.bs, 1, self.ar_u, self.ar_tok)
         d._commit(d.ar_b, n_add=1)
         d.st.x0.copy_(self.ar_tok[:, 0])
         self._cumulate(self.ar_tok, torch.ones_like(self.ar_tok, dtype=torch.bool))
         K.log_append(d.ar_ctr, [(self.ar_tok.view(d.bs), d.ar_log)])
+        if self.grammars is not None:
+            for b, (g, t) in enumerate(zip(self.grammars, self.ar_tok[:, 0].cpu().tolist())):
+                if g is not None and not g.is_terminated():
+                    g.accept_token(int(t))
 
 
 def _any_positive(x) -> bool:

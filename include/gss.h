@@ -210,6 +210,14 @@ typedef struct gss_penalties {
 int gss_penalize_rows(float* logits, int64_t ld_row, int bs, int K, int V, const int32_t* cand,
                       const gss_penalties* pen, gss_stream_t stream);
 
+/* gss_apply_vocab_mask: a grammar's vocabulary mask on logit rows (the grammar backend's apply_vocab_mask, which the
+ * reference calls between the penalties and logit_bias, selfspec_fast_commit.py:186-189; the rows' masks come from
+ * the host walk of fulldraft_bitmask, selfspec_sampling.py:305-337): logits[r * ld_row + v] = -inf where bit v % 32
+ * of mask[r * ld_mask + v / 32] is clear (a set bit allows the token: the packed int32 layout of the grammar
+ * backends' bitmasks). rows <= 65535, ld_mask >= ceil(V / 32). */
+int gss_apply_vocab_mask(float* logits, int64_t ld_row, int rows, int V, const int32_t* mask, int64_t ld_mask,
+                         gss_stream_t stream);
+
 /* gss_sample_rows: target distribution of every row (verify_target_probs, selfspec_sampling.py:266-286): softmax of
  * logits / temperature[b] (temperature <= 0: a point mass at the row maximum), then filter 0 (none), 1 (flashinfer's
  * joint top-k / top-p: token q kept iff #{p > p_q} < top_k[b] and sum{p > p_q} < top_p[b], top_p >= 1 keeping

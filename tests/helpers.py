@@ -32,3 +32,38 @@ def rel_err(out, ref):
     out = out.double().cpu()
     ref = ref.double().cpu()
     return float((out - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+class PositionGrammar:
+    """A grammar object with the serving stack's surface (allocate_vocab_mask, fill_vocab_mask, accept_token,
+    rollback, is_terminated) over a rule that depends on the accepted tokens: after n accepted tokens whose last is
+    x, token t is allowed iff (t + n + x) % 3 != 0. Never terminates."""
+
+    def __init__(self, V, tokens=()):
+        self.V, self.acc = V, list(tokens)
+
+    def allowed(self, t):
+        last = self.acc[-1] if self.acc else 0
+        return (t + len(self.acc) + last) % 3 != 0
+
+    def allocate_vocab_mask(self, vocab_size, batch_size, device):
+        import torch
+        return torch.zeros(batch_size, (vocab_size + 31) // 32, dtype=torch.int32, device=device)
+
+    def fill_vocab_mask(self, mask, idx):
+        import numpy as np
+        import torch
+        bits = np.array([self.allowed(t) for t in range(self.V)] + [False] * (-self.V % 32), dtype=np.uint64)
+        words = (bits.reshape(-1, 32) << np.arange(32, dtype=np.uint64)).sum(1).astype(np.uint32).view(np.int32)
+        mask[idx] = torch.from_numpy(words)
+
+    def accept_token(self, t):
+        if not self.allowed(t):
+            raise ValueError(f"token {t} not allowed")
+        self.acc.append(int(t))
+
+    def rollback(self, k):
+        del self.acc[len(self.acc) - k:]
+
+    def is_terminated(self):
+        return False
