@@ -554,8 +554,12 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
         gemm_epilogue<EPI, false>(p, f0, 0, f, n, s, l16, g4);
       }
   };
-  // two register sets, alternating: while one tile is computed, the next one's weights stream into the other set.
-  // The steady state (two tiles per iteration) always has a next tile, so its loads are issued unconditionally.
+  // Two register sets, alternating: while one tile is computed, the next one's weights stream into the other set.
+  // The steady state (two tiles per iteration) always has a next tile, so its loads are issued unconditionally and
+  // the compiler counts the loads in flight. A workgroup with three tiles (16-feature tiles without the prologue,
+  // whose registers allow a third set) instead issues all three tiles' weights before computing the first: its
+  // compute is small next to a memory round trip, so one wait for everything beats three chained ones.
+  constexpr bool THREE = FT == 1 && PRO == PRO_NONE;
   const int G = gridDim.x;
   const int n_my = (n_tiles - static_cast<int>(blockIdx.x) + G - 1) / G;  // tiles of this workgroup (>= 1)
   auto tile_at = [&](int i) { return static_cast<int>(blockIdx.x) + i * G; };
@@ -582,6 +586,17 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
 #pragma unroll
       for (int u = 0; u < UNR; ++u)
         xb[u][n] = *reinterpret_cast<const u32x4_t*>(xr + min(s_beg + u, ksteps - 1) * 32);
+    }
+  }
+  if constexpr (THREE) {
+    if (n_my == 3) {
+      u32x4_t wc[UNR][FT];
+      load_w(tile_at(1), wb);
+      load_w(tile_at(2), wc);
+      tile(tile_at(0), wa);
+      tile(tile_at(1), wb);
+      tile(tile_at(2), wc);
+      return;
     }
   }
   int i = 0;
