@@ -498,13 +498,24 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
 // of gemm_kernel, so both produce the same bits for the same shape and every row count. With PRO_ADDNORM the
 // workgroup first issues its first tile's weight loads, then builds the normalized activation rows in LDS (the
 // arithmetic of gss_add_rmsnorm, as in gemm_kernel's prologue) while they are in flight.
+//
+// A workgroup with at most FEW_TILES 16-feature tiles (FEW: FT == 1 without the prologue, when the host sized the
+// partials for it) issues every tile's weights at once, runs all their MFMAs, and reduces and finishes all its
+// tiles after one barrier: its compute is small next to a memory round trip, so one wait and one reduction beat a
+// chain of them (gate_up 9216 x 1536 at 17 rows: 10.4 -> 9.8 us per call; staging the activations through LDS on
+// top of it gained nothing).
+constexpr int FEW_TILES = 3;
+
 template <int FT, int NT, int UNR, int EPI, int PRO = PRO_NONE, int E = 8>
-__global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, int ksw, int n_tiles) {
-  extern __shared__ floatx4_t red[];  // [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD]
+__global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, int ksw, int n_tiles, int few) {
+  // LDS: [FEW_TILES or 1][NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD]
+  extern __shared__ floatx4_t red[];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int ksteps = p.Kd / 32;
   const int s_beg = wv * ksw, s_end = min(ksteps, s_beg + ksw);  // ksw <= UNR: one pass
+  constexpr bool FEW = FT == 1 && PRO == PRO_NONE;
+  const int red_sets = FEW && few ? FEW_TILES : 1;
 
   // Every load below is unconditional (clamped indices), so the compiler can count the loads in flight and wait
   // only for the older register set: activation rows past M read row 0 (their outputs are never stored), k-steps
@@ -519,8 +530,7 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
       for (int u = 0; u < UNR; ++u) wa[u][f] = *reinterpret_cast<const u32x4_t*>(wr + min(s_beg + u, ksteps - 1) * 32);
     }
   };
-  auto tile = [&](int t, const u32x4_t(&wa)[UNR][FT]) {
-    floatx4_t acc[FT][NT];
+  auto mfma_tile = [&](const u32x4_t(&wa)[UNR][FT], floatx4_t(&acc)[FT][NT]) {
 #pragma unroll
     for (int f = 0; f < FT; ++f)
 #pragma unroll
@@ -537,37 +547,42 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
                                                                 0, 0);
       }
     }
-    __syncthreads();  // the previous tile's partials have been read
+  };
+  // partials of tile t (in set `set` of the partial area) -> LDS; then its reduction in wave order and epilogue
+  auto post = [&](int set, const floatx4_t(&acc)[FT][NT]) {
 #pragma unroll
     for (int f = 0; f < FT; ++f)
 #pragma unroll
-      for (int n = 0; n < NT; ++n) red[((wv * FT + f) * NT + n) * 64 + lane] = acc[f][n];
-    __syncthreads();
+      for (int n = 0; n < NT; ++n) red[(((set * NW + wv) * FT + f) * NT + n) * 64 + lane] = acc[f][n];
+  };
+  auto finish = [&](int set, int t) {
     const int f0 = t * FT * 16;
 #pragma unroll
     for (int f = 0; f < FT; ++f)
 #pragma unroll
       for (int n = 0; n < NT; ++n) {
-        if ((f * NT + n) % NW != wv || n * 16 + l16 >= p.M || f0 + f * 16 + g4 * 4 >= p.N) continue;
-        floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
-        for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
+        if (((set * FT + f) * NT + n) % NW != wv || n * 16 + l16 >= p.M || f0 + f * 16 + g4 * 4 >= p.N) continue;
+        floatx4_t s = red[(((set * NW + 0) * FT + f) * NT + n) * 64 + lane];
+        for (int v = 1; v < NW; ++v) s += red[(((set * NW + v) * FT + f) * NT + n) * 64 + lane];
         gemm_epilogue<EPI, false>(p, f0, 0, f, n, s, l16, g4);
       }
   };
-  // Two register sets, alternating: while one tile is computed, the next one's weights stream into the other set.
-  // The steady state (two tiles per iteration) always has a next tile, so its loads are issued unconditionally and
-  // the compiler counts the loads in flight. A workgroup with three tiles (16-feature tiles without the prologue,
-  // whose registers allow a third set) instead issues all three tiles' weights before computing the first: its
-  // compute is small next to a memory round trip, so one wait for everything beats three chained ones.
-  constexpr bool THREE = FT == 1 && PRO == PRO_NONE;
+  auto tile = [&](int t, const u32x4_t(&wa)[UNR][FT]) {
+    floatx4_t acc[FT][NT];
+    mfma_tile(wa, acc);
+    __syncthreads();  // the previous tile's partials have been read
+    post(0, acc);
+    __syncthreads();
+    finish(0, t);
+  };
   const int G = gridDim.x;
   const int n_my = (n_tiles - static_cast<int>(blockIdx.x) + G - 1) / G;  // tiles of this workgroup (>= 1)
   auto tile_at = [&](int i) { return static_cast<int>(blockIdx.x) + i * G; };
-  u32x4_t wa[UNR][FT], wb[UNR][FT];
+  u32x4_t wa[UNR][FT], wb[UNR][FT], wc[UNR][FT];  // wc: the few-tile path's third tile
+  uint16_t* xs = reinterpret_cast<uint16_t*>(red + red_sets * NW * FT * NT * 64);
   load_w(tile_at(0), wa);
   if constexpr (PRO == PRO_ADDNORM) {
     // the normalized rows, one wavefront per row, into LDS; workgroup 0 also stores the updated residual
-    uint16_t* xs = reinterpret_cast<uint16_t*>(red + NW * FT * NT * 64);
     for (int r = wv; r < p.M; r += NW) addnorm_row<E>(p, r, lane, xs, blockIdx.x == 0 && p.h_out != nullptr);
     __syncthreads();
 #pragma unroll
@@ -588,17 +603,29 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
         xb[u][n] = *reinterpret_cast<const u32x4_t*>(xr + min(s_beg + u, ksteps - 1) * 32);
     }
   }
-  if constexpr (THREE) {
-    if (n_my == 3) {
-      u32x4_t wc[UNR][FT];
-      load_w(tile_at(1), wb);
-      load_w(tile_at(2), wc);
-      tile(tile_at(0), wa);
-      tile(tile_at(1), wb);
-      tile(tile_at(2), wc);
+  if constexpr (FEW) {
+    if (few) {  // n_my <= FEW_TILES: all weights in flight, all MFMAs, one reduction
+      if (n_my > 1) load_w(tile_at(1), wb);
+      if (n_my > 2) load_w(tile_at(2), wc);
+      floatx4_t acc[FT][NT];
+      mfma_tile(wa, acc);
+      post(0, acc);
+      if (n_my > 1) {
+        mfma_tile(wb, acc);
+        post(1, acc);
+      }
+      if (n_my > 2) {
+        mfma_tile(wc, acc);
+        post(2, acc);
+      }
+      __syncthreads();
+      for (int i = 0; i < n_my; ++i) finish(i, tile_at(i));
       return;
     }
   }
+  // Two register sets, alternating: while one tile is computed, the next one's weights stream into the other set.
+  // The steady state (two tiles per iteration) always has a next tile, so its loads are issued unconditionally and
+  // the compiler counts the loads in flight.
   int i = 0;
   for (; i + 2 < n_my; i += 2) {
     load_w(tile_at(i + 1), wb);
@@ -978,10 +1005,10 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
     const int G = stream_wgs();
     if (p.ksplit == 1 && n_tiles > G) {  // the persistent kernel (same rule as without the prologue)
       switch (p.Kd / 64) {
-        case 4: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 4>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
-        case 8: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 8>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
-        case 16: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 16>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
-        case 24: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 24>), dim3(G), block, lds, st, p, ksw, n_tiles); break;
+        case 4: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 4>), dim3(G), block, lds, st, p, ksw, n_tiles, 0); break;
+        case 8: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 8>), dim3(G), block, lds, st, p, ksw, n_tiles, 0); break;
+        case 16: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 16>), dim3(G), block, lds, st, p, ksw, n_tiles, 0); break;
+        case 24: hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI, PRO, 24>), dim3(G), block, lds, st, p, ksw, n_tiles, 0); break;
         default: return GSS_ERR_UNSUPPORTED;
       }
       return gss_launch_status();
@@ -1000,7 +1027,11 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
       // takes the same kernel): the persistent kernel, one workgroup per CU walking the tiles
       const int G = stream_wgs();
       if (EPI != EPI_PARTS && p.ksplit == 1 && ksw <= 4 && n_tiles > G) {
-        hipLaunchKernelGGL((gemm_stream_kernel<FT, NT, 4, EPI>), dim3(G), block, lds, st, p, ksw, n_tiles);
+        // every workgroup has at most FEW_TILES tiles: partials for all of them (FT = 1: up to 3 x 12 x 4 KB)
+        const int few = FT == 1 && n_tiles <= FEW_TILES * G && lds * FEW_TILES <= MAX_DYN_LDS;
+        constexpr auto k0 = gemm_stream_kernel<FT, NT, 4, EPI>;
+        if (!allow_full_lds<k0>()) return GSS_ERR_LAUNCH;
+        hipLaunchKernelGGL(k0, dim3(G), block, lds * (few ? FEW_TILES : 1), st, p, ksw, n_tiles, few);
         return gss_launch_status();
       }
     }
