@@ -229,11 +229,54 @@ GSS_DEV void post_addnorm_row(const GemmParams& p, int row, int lane) {
   }
 }
 
+// RoPE factors of a lane's 4 output features (two rotated pairs): the position and inverse frequencies are fetched
+// first (rope_fetch, before a kernel's weight loads, so they arrive under them), the bf16-rounded cos / sin computed
+// afterwards (rope_math, while the weights are in flight), so the epilogue has neither a memory round trip nor the
+// transcendental functions on its path. The same expressions as computed in place, so the same bits.
+struct RopeIn {
+  int s0, s1, w, d;  // seq_lens[b], pos_delta[b] (or a stand-in), window row, head dim of the first feature
+  float i0, i1;      // inverse frequencies of the two pairs (clamped index)
+};
+struct RopeCS {
+  float c[2], s[2];
+};
+GSS_DEV RopeIn rope_fetch(const GemmParams& p, int row, int feat) {
+  // loads only, every one unconditional and in bounds (their values are used by rope_math), so no wait is forced
+  // before the loads that follow
+  row = min(row, p.M - 1);  // rows past M are never stored
+  const int b = row / p.W;
+  RopeIn r;
+  r.w = row % p.W;
+  r.d = feat % p.D;
+  const int32_t* pd = p.pos_delta ? p.pos_delta : p.seq_lens;
+  // (no rotated dims: read a valid int instead, never used)
+  const float* fq = p.rot_dim >= 2 ? p.inv_freq : reinterpret_cast<const float*>(p.seq_lens);
+  const int hi = max(p.rot_dim - 2, 0);
+  r.s0 = p.seq_lens[b];
+  r.s1 = pd[b];
+  r.i0 = fq[min(r.d, hi) >> 1];
+  r.i1 = fq[min(r.d + 2, hi) >> 1];
+  return r;
+}
+GSS_DEV RopeCS rope_math(const GemmParams& p, const RopeIn& r) {
+  const int pos = r.s0 + (p.pos_delta ? r.s1 : 0) + r.w;
+  const float fr0 = static_cast<float>(pos) * (r.d < p.rot_dim ? r.i0 : 0.f);
+  const float fr1 = static_cast<float>(pos) * (r.d + 2 < p.rot_dim ? r.i1 : 0.f);
+  RopeCS cs;
+  cs.c[0] = round_bf16(cosf(fr0));
+  cs.s[0] = round_bf16(sinf(fr0));
+  cs.c[1] = round_bf16(cosf(fr1));
+  cs.s[1] = round_bf16(sinf(fr1));
+  return cs;
+}
+
 // Epilogue of output tile (f, n) of the workgroup whose first feature is f0 and first row row0, on its reduced sum s
 // (lane: activation row row0 + n*16 + l16, features f0 + f*16 + g4*4 .. +3). The GEMM output is rounded to bf16
-// first, as a bf16 torch linear writes it.
+// first, as a bf16 torch linear writes it. EPI_ROPE takes the lane's precomputed factors if given (pre), else
+// computes them here.
 template <int EPI, bool POST>
-GSS_DEV void gemm_epilogue(const GemmParams& p, int f0, int row0, int f, int n, floatx4_t s, int l16, int g4) {
+GSS_DEV void gemm_epilogue(const GemmParams& p, int f0, int row0, int f, int n, floatx4_t s, int l16, int g4,
+                           const RopeCS* pre = nullptr) {
   const int row = row0 + n * 16 + l16;     // activation row
   const int feat = f0 + f * 16 + g4 * 4;   // first of this lane's 4 consecutive output features
   float y0 = s[0], y1 = s[1], y2 = s[2], y3 = s[3];
@@ -256,16 +299,14 @@ GSS_DEV void gemm_epilogue(const GemmParams& p, int f0, int row0, int f, int n, 
     *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.y) + static_cast<int64_t>(row) * p.ldy + feat / 2) =
         pack_bf16x2(u0 * s0, u1 * s1);
   } else {  // EPI_ROPE
-    const int b = row / p.W, w = row % p.W;
     const int head = feat / p.D, d = feat % p.D;  // 4 features never straddle a head (D % 16 == 0)
     float o[4] = {round_bf16(y0), round_bf16(y1), round_bf16(y2), round_bf16(y3)};
     if (head < p.Hq + p.Hkv) {
-      const int pos = p.seq_lens[b] + (p.pos_delta ? p.pos_delta[b] : 0) + w;
+      const RopeCS cs = pre ? *pre : rope_math(p, rope_fetch(p, row, feat));
 #pragma unroll
       for (int e = 0; e < 4; e += 2) {
         if (d + e < p.rot_dim) {
-          const float fr = static_cast<float>(pos) * p.inv_freq[(d + e) >> 1];
-          const float c = round_bf16(cosf(fr)), sn = round_bf16(sinf(fr));
+          const float c = cs.c[e >> 1], sn = cs.s[e >> 1];
           const float x0 = o[e], x1 = o[e + 1];
           o[e] = round_bf16(round_bf16(x0 * c) - round_bf16(x1 * sn));
           o[e + 1] = round_bf16(round_bf16(x1 * c) + round_bf16(x0 * sn));
@@ -318,6 +359,27 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
     xlive[n] = r < Ms;
     xrow[n] = xs0 + static_cast<int64_t>(xlive[n] ? r : 0) * p.ldx + g4 * 8;
   }
+
+  // RoPE factors of the output tiles this wave finishes ((f * NT + n) % NW == wv): fetched before any other load (so
+  // they arrive under the weights), computed after the MFMAs
+  RopeIn rin[FT][NT];
+  RopeCS rcs[FT][NT];
+  auto owns = [&](int f, int n) { return (f * NT + n) % NW == wv; };
+  if constexpr (EPI == EPI_ROPE) {
+#pragma unroll
+    for (int f = 0; f < FT; ++f)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) rin[f][n] = rope_fetch(p, row0 + n * 16 + l16, f0 + f * 16 + g4 * 4);
+  }
+  auto rope_prepare = [&]() {
+    if constexpr (EPI == EPI_ROPE) {
+#pragma unroll
+      for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          if (owns(f, n)) rcs[f][n] = rope_math(p, rin[f][n]);
+    }
+  };
 
   uint16_t* xs = reinterpret_cast<uint16_t*>(red + NW * FT * NT * 64);
   const int cpr = ksw * 4;
@@ -398,6 +460,8 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
     }
   }
 
+  rope_prepare();  // (inside the load pass, the compiler hoists it above the weight loads)
+
   // ---- reduce the NW wave partials in wave order --------------------------------------------------------------
 #pragma unroll
   for (int f = 0; f < FT; ++f)
@@ -406,7 +470,9 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   __syncthreads();
 
   // epilogue of tile (f, n) on its reduced sum (wave v owns the tiles with (f * NT + n) % NW == v)
-  auto epilogue = [&](int f, int n, floatx4_t s) { gemm_epilogue<EPI, POST>(p, f0, row0, f, n, s, l16, g4); };
+  auto epilogue = [&](int f, int n, floatx4_t s) {
+    gemm_epilogue<EPI, POST>(p, f0, row0, f, n, s, l16, g4, EPI == EPI_ROPE ? &rcs[f][n] : nullptr);
+  };
   auto reduced = [&](int f, int n) {
     floatx4_t s = red[((0 * FT + f) * NT + n) * 64 + lane];
     for (int v = 1; v < NW; ++v) s += red[((v * FT + f) * NT + n) * 64 + lane];
