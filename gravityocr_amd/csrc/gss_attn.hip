@@ -7,10 +7,11 @@
 //     share every K/V byte read (row n = w*G + g); rows are MFMA N-tiles of 16. One workgroup takes a unit
 //     (sequence, kv head, key split) for all its rows (up to 10 N-tiles; wider windows use several row groups), so
 //     each K/V byte of the split enters the CU's LDS once.
-//   * Waves are (row wave, key lane) pairs, up to 4 x 2: a row wave owns NGW <= 3 N-tiles (Q fragments in
-//     registers), key lane kl takes key half kl (32 keys) of every tile of the split. Each wave runs its own online
-//     softmax, so no data moves between waves until the end, where the two key lanes of a row wave combine in lane
-//     order (fp32).
+//   * Wide kernel (batches): up to 4 row waves, each owning NGW <= 3 N-tiles (Q fragments in registers) and scoring
+//     every tile of the split in two 32-key steps with its own online softmax, so no data moves between waves; two
+//     workgroups share a CU, so their tile loops interleave on the SIMDs (the waves of one workgroup meet at a
+//     barrier every tile and would otherwise run their MFMA and softmax phases in lockstep). The row-group kernel
+//     (small batches) splits each stage's keys over its waves instead and combines them at the end.
 //   * Transposed contractions on v_mfma_f32_16x16x32_bf16:  S^T = K Q^T  (M = tokens, N = rows, K = head dim) and
 //     O^T = V^T P^T  (M = head dim, N = rows, K = tokens). A lane then owns one query row per N-tile, so the online
 //     softmax max is two xor-shuffles and the row sum stays lane-local until the end. The P^T operand is the lane's
@@ -19,15 +20,15 @@
 //   * K tiles live in LDS as [token][D] with an XOR swizzle of the 16-byte chunks (conflict-free 16-row reads);
 //     V pages are stored token-minor ([D][16] per page) in HBM, so the V^T operand is two 8-byte LDS reads.
 //   * Tiles stream straight from global memory into LDS (global_load_lds_dwordx4; no staging registers) through a
-//     ring of 4 one-tile slots: tiles i + 1 .. i + 3 are in flight while tile i is computed, one workgroup barrier
-//     per tile, and each wave waits for exactly its own loads of tile i (vmcnt counts in issue order). The loads
-//     are issued from inline assembly so the compiler does not add a wait for every in-flight LDS load before each
-//     LDS read, which would serialize the ring. The split's page ids are read once into LDS.
+//     ring of 2 one-tile slots per workgroup: tile i + 1 is in flight while tile i is computed (and the CU's other
+//     workgroup streams its own), one workgroup barrier per tile, each wave waiting for its own loads of tile i. The
+//     loads are issued from inline assembly so the compiler does not add a wait for every in-flight LDS load before
+//     each LDS read. The split's page ids are read once into LDS.
 //   * Grid order is XCD-aware: the grid enumerates only the units that hold keys (each workgroup finds its unit from
 //     the device-side lengths), consecutive units go to different XCDs (ragged batches balance), the row groups of
 //     one unit to the same XCD (their repeated K/V reads hit its L2).
 //   * Keys are tiled by absolute position (window rows take the positions after the prefix); the split size, the
-//     tile -> split -> key lane assignment and the kernel come from the caller's plan (gss_attn_plan) only, never
+//     tile -> split -> wave assignment and the kernel come from the caller's plan (gss_attn_plan) only, never
 //     from W, the prefix length or the row grouping, and every combine runs in a fixed order. Results therefore do not
 //     depend on where a key comes from or on how many rows are in the window: a verify row reproduces the AR step
 //     of the same token bit for bit. With several splits, the normalized partial O (bf16) and (m, l) (fp32) of each
@@ -40,7 +41,6 @@ namespace {
 
 constexpr int PAGE = 16;
 constexpr int TILE = 64;        // KV tokens per tile (4 pages)
-constexpr int KL = 2;           // key lanes: tile j of a split is scored by the waves of lane j % KL
 constexpr int RW_MAX = 4;       // row waves per workgroup: <= 8 waves, 2 per SIMD
 constexpr int NGW_MAX = 3;      // N-tiles (16 query rows) per row wave
 constexpr int MAX_TPS = 256;    // tiles per split (page ids of a split in LDS: 4 * MAX_TPS ints)
@@ -75,16 +75,13 @@ struct AttnParams {
 };
 
 template <int D>
-struct Lds {
+struct Lds {  // the wide kernel: a 2-slot ring and the split's page ids, so two workgroups fit a CU
   static constexpr int TILE_EL = TILE * D;          // elements of one K (or V) tile
-  static constexpr int NSLOT = 4;                   // one-tile slots of the load ring
+  static constexpr int NSLOT = 2;                   // one-tile slots of the load ring
   static constexpr int SLOT_EL = 2 * TILE_EL;       // a slot: K [TILE][D] swizzled, then V [4][D][16]
   static constexpr int BUF_BYTES = NSLOT * SLOT_EL * 2;  // the ring (bytes)
   static constexpr int TOTAL = BUF_BYTES + 4 * MAX_TPS * 4;  // then the split's page ids (4 pages per tile)
-  // combine scratch (reuses the stage buffers): per (row wave, key lane >= 1, N-tile) O^T fp32 and (m, l) of 16 rows
-  static constexpr int SCR_FLOATS = (D / 16) * 256 + 32;
-  static_assert(RW_MAX * (KL - 1) * NGW_MAX * SCR_FLOATS * 4 <= BUF_BYTES, "combine scratch exceeds the buffers");
-  static_assert(TOTAL <= 160 * 1024, "LDS budget");
+  static_assert(2 * TOTAL <= 160 * 1024, "two workgroups per CU");
 };
 
 template <int D>
@@ -205,12 +202,13 @@ GSS_DEV int valid_splits(int L, int W, int tps) {
 }
 
 template <int D, int NGW, int RWT>
-__global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p) {
-  constexpr int NW = KL * RWT;  // waves per workgroup
+__global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
+  using LY = Lds<D>;
+  constexpr int NW = RWT;  // waves per workgroup: one per row wave
   constexpr int KS = D / 32;   // MFMA K-steps over the head dim
   constexpr int DT = D / 16;   // 16-row tiles of the head dim (O^T M-tiles)
   constexpr int CH = D / 8;    // 16-byte chunks per K row
-  constexpr int TILE_EL = Lds<D>::TILE_EL;
+  constexpr int TILE_EL = LY::TILE_EL;
   constexpr int TILE_INSTR = TILE * CH / 64;    // direct-load instructions per K (or V) tile
   constexpr int PAGE_INSTR = PAGE * CH / 64;    // instructions per (page, head) block of K (or V)
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -267,7 +265,7 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   const int b = __builtin_amdgcn_readfirstlane(s_unit[0]), kvh = __builtin_amdgcn_readfirstlane(s_unit[1]),
             s = __builtin_amdgcn_readfirstlane(s_unit[2]);
   if (b < 0) return;  // past the last valid unit
-  const int kl = wv % KL, rw = wv / KL;                       // key lane, row wave
+  const int rw = wv;  // row wave
   const int l16 = lane & 15, g4 = lane >> 4;
   // committed prefix length; clamped to the plan's capacity and to what the page-table row can address, so every
   // key falls in one of the plan's splits and every page-table read is in bounds
@@ -292,7 +290,7 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   __builtin_assume(ng >= NGW - 1 && ng <= NGW);  // the host deals NGW or NGW - 1 tiles to every row wave
   const int nt0 = rg * p.TPG + rw * tb_base + min(rw, tb_extra);
   // the split's page ids -> LDS, once; issued right after the query loads, so both are in flight together
-  int* spages = reinterpret_cast<int*>(reinterpret_cast<char*>(smem) + Lds<D>::BUF_BYTES);
+  int* spages = reinterpret_cast<int*>(reinterpret_cast<char*>(smem) + LY::BUF_BYTES);
   auto load_pages = [&]() {
     for (int i = tid; i < (t_end - t_beg) * (TILE / PAGE); i += blockDim.x) {
       const int pos = t_beg * TILE + i * PAGE;
@@ -304,12 +302,10 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
   // instruction's LDS base + 16 i) into a ring of NSLOT one-tile slots, each K [TILE][D] (XOR-swizzled 16-byte
   // chunks) then V [4 pages][D][16]. Every instruction covers 64 chunks of one (page, head) block, so its page id is
   // wave-uniform. Loads are unconditional: pages past the prefix read page 0 (in bounds) and the boundary fix
-  // overwrites those positions, so every wave issues exactly `per_tile` instructions per tile and the wait for tile
-  // i is an exact count of the loads issued after it.
-  constexpr int NSLOT = Lds<D>::NSLOT;
-  const int per_tile = (2 * TILE_INSTR - wv + NW - 1) / NW;  // this wave's instructions per tile
+  // overwrites those positions.
+  constexpr int NSLOT = LY::NSLOT;
   auto issue_tile = [&](int i) {  // tile t_beg + i of the split -> slot i % NSLOT
-    uint16_t* buf = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
+    uint16_t* buf = smem + (i % NSLOT) * LY::SLOT_EL;
     const int pgv = lane < TILE / PAGE ? spages[i * (TILE / PAGE) + lane] : 0;
 #pragma unroll 1  // unrolled, the per-instruction lane offsets are hoisted out of the tile loop and spilled
     for (int k = 0; k < (2 * TILE_INSTR + NW - 1) / NW; ++k) {
@@ -331,34 +327,19 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
       dma16((is_v ? vp_head : kp_head) + page * page_stride + off, buf + (is_v ? TILE_EL : 0) + ib * 512);
     }
   };
-  // wait until this wave's loads of the tile `ahead` tiles before the newest one issued have landed (vmcnt counts
-  // in issue order; the count is an immediate, hence the switch)
-  auto wait_tile = [&](int ahead) {
-    switch (ahead * per_tile) {
-#define GSS_VMW(n) \
-  case n:          \
-    asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory"); \
-    break;
-      GSS_VMW(1) GSS_VMW(2) GSS_VMW(3) GSS_VMW(4) GSS_VMW(5) GSS_VMW(6) GSS_VMW(8) GSS_VMW(10) GSS_VMW(12)
-      GSS_VMW(16) GSS_VMW(24) GSS_VMW(32)
-#undef GSS_VMW
-      default:
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-  };
   // Tile i reaching past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
   // and the V chunk that straddles L keeps only its prefix tokens.
   auto fix_tile = [&](int i) {
     const int t = t_beg + i;
     if ((t + 1) * TILE <= L) return false;
-    uint16_t* lds_k = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
+    uint16_t* lds_k = smem + (i % NSLOT) * LY::SLOT_EL;
     fix_boundary<D, true>(lds_k, lds_k + TILE_EL, t, t, t + 1, L, W, p.k_win, p.v_win, win_base, p.Hkv, tid,
                           blockDim.x);
     return true;
   };
   const int hsw = (l16 >> 3) & 1;  // the V half swap of head dims d with bit 3 set (d = dt*16 + l16)
   const int vrd = ((g4 >> 1) ^ hsw) * 8 + (g4 & 1) * 4;
-  const int hh = kl;               // this wave's key half of every tile
+  
   const int n_t = t_end - t_beg;
 
   // The wave's work for its NG N-tiles, NG a compile-time count (NGW or NGW - 1, dealt by the host), so the MFMA
@@ -393,13 +374,13 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
       }
     __syncthreads();
 
-    // ---- online softmax, private to the wave: key lane kl takes key half kl (32 keys, m-tiles 2 kl and 2 kl + 1)
-    // of every tile of the split, for its NG N-tiles. Scores come out of the MFMA in the log2 domain (the queries
-    // are pre-scaled). Each row keeps a reference max m that trails its running max by at most RESCALE_SLACK, and
-    // P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more than the slack
-    // (rare after the first tiles) does the wave take the row maxima (two xor-shuffles over the row's lanes), move
-    // the references and rescale O and l. P^T is packed to bf16 in the lane that scored it, and O^T += V^T P^T over
-    // one K-step of 32 keys.
+    // ---- online softmax, private to the wave: it scores the two key halves hh of every tile of the split (32
+    // keys, m-tiles 2 hh and 2 hh + 1, one step each) for its NG N-tiles. Scores come out of the MFMA in the log2
+    // domain (the queries are pre-scaled). Each row keeps a reference max m that trails its running max by at most
+    // RESCALE_SLACK, and P^T = 2^(s - m) <= 2^RESCALE_SLACK; only when some row's max exceeds its reference by more
+    // than the slack (rare after the first tiles) does the wave take the row maxima (two xor-shuffles over the row's
+    // lanes), move the references and rescale O and l. P^T is packed to bf16 in the lane that scored it, and
+    // O^T += V^T P^T over one K-step of 32 keys.
     floatx4_t o[NG][DT];
     float m_run[NG], l_run[NG];
 #pragma unroll
@@ -413,158 +394,126 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
     // at the loop header would make it wait for every vector memory operation inside the loop, the prefetched tiles
     // included (a real s_waitcnt, which the compiler's wait insertion accounts for)
     __builtin_amdgcn_s_waitcnt(0);
-    for (int i = 0; i < min(NSLOT - 1, n_t); ++i) issue_tile(i);
+    static_assert(NSLOT == 2, "one tile in flight: the wait below is for every load");
+    issue_tile(0);
     for (int i = 0; i < n_t; ++i) {
-      wait_tile(min(NSLOT - 2, n_t - 1 - i));  // this wave's loads of tile i
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's loads of tile i (the only ones in flight)
       __syncthreads();  // every wave's loads of tile i have landed; every wave is done with tile i - 1's slot
       if (fix_tile(i)) __syncthreads();  // block-uniform condition
       if (i + NSLOT - 1 < n_t) issue_tile(i + NSLOT - 1);  // into the slot of tile i - 1
       const int tb = (t_beg + i) * TILE;
-      const uint16_t* tk = smem + (i % NSLOT) * Lds<D>::SLOT_EL;
+      const uint16_t* tk = smem + (i % NSLOT) * LY::SLOT_EL;
       const uint16_t* tv = tk + TILE_EL;
-      // scores: the half's K fragments (2 m-tiles x KS K-steps) are read in two batches, the second in flight
-      // under the first batch's MFMAs; K-step outer and m-tile inner, each accumulator over the K-steps in order
-      floatx4_t sacc[NG][2];
+#pragma unroll 1
+      for (int hh = 0; hh < 2; ++hh) {  // the tile's two key halves (32 keys each), one online-softmax step each
+        // scores: the half's K fragments (2 m-tiles x KS K-steps) are read in two batches, the second in flight
+        // under the first batch's MFMAs; K-step outer and m-tile inner, each accumulator over the K-steps in order
+        floatx4_t sacc[NG][2];
 #pragma unroll
-      for (int g = 0; g < NG; ++g) sacc[g][0] = sacc[g][1] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-      constexpr int KB = KS;  // fragments per batch (i2 = ks * 2 + mt)
-      auto kfrag = [&](int i2) {
-        return *reinterpret_cast<const bf16x8_t*>(&tk[k_lds_index<D>((2 * hh + (i2 & 1)) * 16 + l16, (i2 >> 1) * 4 + g4)]);
-      };
-      bf16x8_t kf[2][KB];
+        for (int g = 0; g < NG; ++g) sacc[g][0] = sacc[g][1] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        constexpr int KB = KS;  // fragments per batch (i2 = ks * 2 + mt)
+        auto kfrag = [&](int i2) {
+          return *reinterpret_cast<const bf16x8_t*>(
+              &tk[k_lds_index<D>((2 * hh + (i2 & 1)) * 16 + l16, (i2 >> 1) * 4 + g4)]);
+        };
+        bf16x8_t kf[2][KB];
 #pragma unroll
-      for (int j = 0; j < KB; ++j) kf[0][j] = kfrag(j);
+        for (int j = 0; j < KB; ++j) kf[0][j] = kfrag(j);
 #pragma unroll
-      for (int bt = 0; bt < 2; ++bt) {
-        if (bt == 0) {
+        for (int bt = 0; bt < 2; ++bt) {
+          if (bt == 0) {
 #pragma unroll
-          for (int j = 0; j < KB; ++j) kf[1][j] = kfrag(KB + j);
+            for (int j = 0; j < KB; ++j) kf[1][j] = kfrag(KB + j);
+          }
+#pragma unroll
+          for (int j = 0; j < KB; ++j) {
+            const int i2 = bt * KB + j;
+#pragma unroll
+            for (int g = 0; g < NG; ++g)
+              sacc[g][i2 & 1] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[bt][j], qf[g][i2 >> 1], sacc[g][i2 & 1], 0, 0, 0);
+          }
         }
+        // the V^T fragments do not depend on the scores: the first half is read now, under the softmax, the rest
+        // under the first half's MFMAs
+        bf16x8_t vf[DT];
+        auto vfrag = [&](int dt) {
+          const int d = dt * 16 + l16;
+          const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh) * D + d) * PAGE + vrd]);
+          const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh + 1) * D + d) * PAGE + vrd]);
+          return __builtin_bit_cast(bf16x8_t, u32x4_t{v0[0], v0[1], v1[0], v1[1]});
+        };
 #pragma unroll
-        for (int j = 0; j < KB; ++j) {
-          const int i2 = bt * KB + j;
+        for (int dt = 0; dt < DT / 2; ++dt) vf[dt] = vfrag(dt);
+        if (tb + TILE > L) {  // keys past the prefix: the window mask (wave-uniform branch)
 #pragma unroll
-          for (int g = 0; g < NG; ++g)
-            sacc[g][i2 & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[bt][j], qf[g][i2 >> 1], sacc[g][i2 & 1], 0, 0, 0);
+          for (int g = 0; g < NG; ++g) {
+            const int n = (nt0 + g) * 16 + l16;
+            const int roww = (n < p.R ? n : 0) / p.G;  // the row's window index
+#pragma unroll
+            for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int pos = tb + (2 * hh + mt) * 16 + g4 * 4 + e;
+                const int wj = pos - L;
+                const bool vis = pos < L || (wj < W && (roww >= nc || wj <= roww));
+                if (!vis) sacc[g][mt][e] = -INFINITY;
+              }
+          }
         }
-      }
-      // the V^T fragments do not depend on the scores: the first half is read now, under the softmax, the rest
-      // under the first half's MFMAs
-      bf16x8_t vf[DT];
-      auto vfrag = [&](int dt) {
-        const int d = dt * 16 + l16;
-        const u32x2_t v0 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh) * D + d) * PAGE + vrd]);
-        const u32x2_t v1 = *reinterpret_cast<const u32x2_t*>(&tv[((2 * hh + 1) * D + d) * PAGE + vrd]);
-        return __builtin_bit_cast(bf16x8_t, u32x4_t{v0[0], v0[1], v1[0], v1[1]});
-      };
-#pragma unroll
-      for (int dt = 0; dt < DT / 2; ++dt) vf[dt] = vfrag(dt);
-      if (tb + TILE > L) {  // keys past the prefix: the window mask (wave-uniform branch)
+        bf16x8_t pb[NG];
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-          const int n = (nt0 + g) * 16 + l16;
-          const int roww = (n < p.R ? n : 0) / p.G;  // the row's window index
+          // the lane's own max over its 8 scores of the row; a row's reference moves only when its max exceeds it by
+          // more than the slack (or on its first visible keys, m_run = -inf), so the row max over the row's 4 lanes
+          // (two xor-shuffles) is needed only when some lane's own max does: the wave votes first. Keys that are all
+          // masked (mx = -inf) never move a reference.
+          float mx = fmaxf(fmaxf(fmaxf(sacc[g][0][0], sacc[g][0][1]), fmaxf(sacc[g][0][2], sacc[g][0][3])),
+                           fmaxf(fmaxf(sacc[g][1][0], sacc[g][1][1]), fmaxf(sacc[g][1][2], sacc[g][1][3])));
+          if (__any(mx > m_run[g] + RESCALE_SLACK)) {  // wave-uniform: rescale O and l of the rows that moved
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float m_new = mx > m_run[g] + RESCALE_SLACK ? mx : m_run[g];
+            // 1 for rows that keep their reference (also -inf: no visible key yet, where -inf - -inf would be NaN),
+            // 0 on a row's first visible keys
+            const float alpha = m_new == m_run[g] ? 1.f : fast_exp2(m_run[g] - m_new);
+            m_run[g] = m_new;
+            l_run[g] *= alpha;
 #pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
+            for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * alpha;
+          }
+          const float m_use = m_run[g] == -INFINITY ? 0.f : m_run[g];  // a row with no visible key yet: P = 0
+          uint32_t pk[4];
+          float ls = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int pos = tb + (2 * hh + mt) * 16 + g4 * 4 + e;
-              const int wj = pos - L;
-              const bool vis = pos < L || (wj < W && (roww >= nc || wj <= roww));
-              if (!vis) sacc[g][mt][e] = -INFINITY;
-            }
+          for (int j = 0; j < 4; ++j) {
+            const floatx4_t& sv = sacc[g][j >> 1];
+            const float p0 = fast_exp2(sv[(2 * j) & 3] - m_use);
+            const float p1 = fast_exp2(sv[(2 * j + 1) & 3] - m_use);
+            ls += p0 + p1;
+            pk[j] = cvt_pk_bf16(p0, p1);
+          }
+          l_run[g] += ls;
+          pb[g] = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
         }
+#pragma unroll
+        for (int dt = DT / 2; dt < DT; ++dt) vf[dt] = vfrag(dt);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int g = 0; g < NG; ++g)
+            o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt], pb[g], o[g][dt], 0, 0, 0);
       }
-      bf16x8_t pb[NG];
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        // the lane's own max over its 8 scores of the row; a row's reference moves only when its max exceeds it by
-        // more than the slack (or on its first visible keys, m_run = -inf), so the row max over the row's 4 lanes
-        // (two xor-shuffles) is needed only when some lane's own max does: the wave votes first. Keys that are all
-        // masked (mx = -inf) never move a reference.
-        float mx = fmaxf(fmaxf(fmaxf(sacc[g][0][0], sacc[g][0][1]), fmaxf(sacc[g][0][2], sacc[g][0][3])),
-                         fmaxf(fmaxf(sacc[g][1][0], sacc[g][1][1]), fmaxf(sacc[g][1][2], sacc[g][1][3])));
-        if (__any(mx > m_run[g] + RESCALE_SLACK)) {  // wave-uniform: rescale O and l of the rows that moved
-          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-          const float m_new = mx > m_run[g] + RESCALE_SLACK ? mx : m_run[g];
-          // 1 for rows that keep their reference (also -inf: no visible key yet, where -inf - -inf would be NaN),
-          // 0 on a row's first visible keys
-          const float alpha = m_new == m_run[g] ? 1.f : fast_exp2(m_run[g] - m_new);
-          m_run[g] = m_new;
-          l_run[g] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * alpha;
-        }
-        const float m_use = m_run[g] == -INFINITY ? 0.f : m_run[g];  // a row with no visible key yet: P = 0
-        uint32_t pk[4];
-        float ls = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const floatx4_t& sv = sacc[g][j >> 1];
-          const float p0 = fast_exp2(sv[(2 * j) & 3] - m_use);
-          const float p1 = fast_exp2(sv[(2 * j + 1) & 3] - m_use);
-          ls += p0 + p1;
-          pk[j] = cvt_pk_bf16(p0, p1);
-        }
-        l_run[g] += ls;
-        pb[g] = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
-      }
-#pragma unroll
-      for (int dt = DT / 2; dt < DT; ++dt) vf[dt] = vfrag(dt);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int g = 0; g < NG; ++g) o[g][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[dt], pb[g], o[g][dt], 0, 0, 0);
     }
 
-    // ---- combine the KL key lanes of each row wave in lane order (fp32, through LDS), normalize, write.
+    // ---- the wave's rows: the row sums over the 4 lane groups, then O / l (bf16) and (m, l), or the output
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       l_run[g] += __shfl_xor(l_run[g], 16, 64);
       l_run[g] += __shfl_xor(l_run[g], 32, 64);
-    }
-    __syncthreads();  // every wave is done with the stage buffers: reuse them as scratch
-    float* scr = reinterpret_cast<float*>(smem);
-    // slot of (row wave, key lane k >= 1, N-tile g): O^T [DT][64 lanes] x 4, then m [16 rows], l [16 rows]
-    auto slot = [&](int k, int g) {
-      return scr + static_cast<size_t>((rw * (KL - 1) + k - 1) * NGW + g) * Lds<D>::SCR_FLOATS;
-    };
-    if (kl != 0) {
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        float* sl = slot(kl, g);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) reinterpret_cast<floatx4_t*>(sl)[dt * 64 + lane] = o[g][dt];
-        if (g4 == 0) {
-          sl[DT * 256 + l16] = m_run[g];
-          sl[DT * 256 + 16 + l16] = l_run[g];
-        }
-      }
-    }
-    __syncthreads();
-    if (kl != 0) return;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
       const int n = (nt0 + g) * 16 + l16;
-      float M = m_run[g];
-#pragma unroll
-      for (int k = 1; k < KL; ++k) M = fmaxf(M, slot(k, g)[DT * 256 + l16]);
-      const float Mu = M == -INFINITY ? 0.f : M;
-      const float a0 = fast_exp2(m_run[g] - Mu);
-      float lc = l_run[g] * a0;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[g][dt] = o[g][dt] * a0;
-#pragma unroll
-      for (int k = 1; k < KL; ++k) {
-        const float* sl = slot(k, g);
-        const float ak = fast_exp2(sl[DT * 256 + l16] - Mu);
-        lc += sl[DT * 256 + 16 + l16] * ak;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[g][dt] += reinterpret_cast<const floatx4_t*>(sl)[dt * 64 + lane] * ak;
-      }
       if (n >= p.R) continue;
-      const float inv = lc > 0.f ? 1.f / lc : 0.f;
+      const float inv = l_run[g] > 0.f ? 1.f / l_run[g] : 0.f;
       uint16_t* orow;
       if (p.n_split == 1) {
         orow = p.out + ((static_cast<int64_t>(b) * W + n / p.G) * p.Hq + kvh * p.G + n % p.G) * D;
@@ -573,14 +522,14 @@ __global__ void __launch_bounds__(64 * KL * RWT) attn_split_kernel(AttnParams p)
         orow = p.ws_o + ((static_cast<int64_t>(b) * p.Hkv + kvh) * p.n_split + s) * p.R * D +
                static_cast<int64_t>(n) * D;
         if (g4 == 0) {
-          p.ws_ml[(rowid * p.n_split + s) * 2 + 0] = M;
-          p.ws_ml[(rowid * p.n_split + s) * 2 + 1] = lc;
+          p.ws_ml[(rowid * p.n_split + s) * 2 + 0] = m_run[g];
+          p.ws_ml[(rowid * p.n_split + s) * 2 + 1] = l_run[g];
         }
       }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
-        *reinterpret_cast<u32x2_t*>(orow + dt * 16 + g4 * 4) =
-            u32x2_t{cvt_pk_bf16(o[g][dt][0] * inv, o[g][dt][1] * inv), cvt_pk_bf16(o[g][dt][2] * inv, o[g][dt][3] * inv)};
+        *reinterpret_cast<u32x2_t*>(orow + dt * 16 + g4 * 4) = u32x2_t{
+            cvt_pk_bf16(o[g][dt][0] * inv, o[g][dt][1] * inv), cvt_pk_bf16(o[g][dt][2] * inv, o[g][dt][3] * inv)};
     }
   };
   static_assert(NGW >= 2, "row waves take NGW or NGW - 1 >= 1 N-tiles");
@@ -1033,7 +982,7 @@ int launch_d(const AttnParams& p, int bs, bool wide, int ng, hipStream_t st) {
   if (set_lds_limits<D>() != GSS_OK) return GSS_ERR_LAUNCH;
   const dim3 grid((p.n_units + 7) / 8 * 8 * p.RG);
   if (wide) {
-    const dim3 block(64 * KL * p.RW);
+    const dim3 block(64 * p.RW);
     constexpr size_t lds = Lds<D>::TOTAL;
     // row waves x N-tiles per row wave: 1..4 x <= 2 (one N-tile per wave runs on the two-tile instantiation, only
     // its first tile computed), or 4 x 3
