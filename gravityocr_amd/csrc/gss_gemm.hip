@@ -1027,19 +1027,25 @@ int launch_tiled_cfg(GemmParams& p, int ksw, hipStream_t st) {
 
 // The tiled kernel for M > 64, by how many blocks each tiling makes (any tiling computes the same bits; only the
 // speed depends on it): 256 x 128 blocks of 8 waves (64 x 64 per wave, two waves per SIMD, a 3-deep ring of
-// 2-k-step chunks) when they give every CU a workgroup (not with several splits folded in the kernel: the extra
-// accumulators would spill), else 128 x 128 blocks of 8 waves (32 x 64 per wave), else 64 x 64 blocks of 4 waves
-// (two workgroups per CU). Measured on the decoder's shapes: the 256 x 128 blocks run the 8192-row gate_up
-// (9216 x 1536) at 340 us against 480 us for 128 x 128 blocks of 4 waves; at 544 rows the 8-wave 128 x 128 blocks
-// take 45 us against 57 us (4 waves) and 49 us (64 x 64). p.ksplit / p.kps / the wave range ksw are gemm_kernel's
-// for the same (N, Kd).
+// 2-k-step chunks) when they give about two thirds of the CUs a workgroup (not with several splits folded in the
+// kernel: the extra accumulators would spill), else 128 x 128 blocks of 8 waves (32 x 64 per wave) by the same
+// rule, else 64 x 64 blocks of 4 waves (two workgroups per CU). Measured on the decoder's shapes: the 256 x 128
+// blocks run the 8192-row gate_up (9216 x 1536) at 340 us against 480 us for 128 x 128 blocks of 4 waves; at 544
+// rows gate_up takes 36 us on 256 x 128 blocks (180 workgroups) against 43 us on 128 x 128 (360); at 288 rows 23 us
+// on 128 x 128 (216) against 28 us on 64 x 64; at 1056 rows qkv / o_proj / down_proj take 28 / 18 / 31 us on
+// 128 x 128 against 32 / 23 / 40 us on 64 x 64, while qkv at 544 rows stays faster on 64 x 64 (360 workgroups) than
+// on 128 x 128 (100): 19.6 against 28 us. p.ksplit / p.kps / the wave range ksw are gemm_kernel's for the same
+// (N, Kd).
 template <int EPI>
 int launch_tiled(GemmParams& p, int ksw, hipStream_t st) {
   const int z = EPI == EPI_PARTS ? p.ksplit : 1;
   const bool multi = EPI != EPI_PARTS && p.ksplit > 1;
   auto blocks = [&](int bf, int bm) { return static_cast<int64_t>((p.N + bf - 1) / bf) * ((p.M + bm - 1) / bm) * z; };
-  if (!multi && blocks(256, 128) >= stream_wgs()) return launch_tiled_k<EPI, 4, 2, 4, 4, 2, 3, false>(p, ksw, st);
-  if (blocks(128, 128) >= stream_wgs()) return launch_tiled_cfg<EPI, 4, 2, 2, 4, 4, 2>(p, ksw, st);
+  // the largest block that still gives about two thirds of the CUs a workgroup (bigger blocks reuse each LDS byte
+  // for more MFMAs; below that, idle CUs cost more than the reuse gains)
+  const int64_t enough = (2 * stream_wgs() + 2) / 3;
+  if (!multi && blocks(256, 128) >= enough) return launch_tiled_k<EPI, 4, 2, 4, 4, 2, 3, false>(p, ksw, st);
+  if (blocks(128, 128) >= enough) return launch_tiled_cfg<EPI, 4, 2, 2, 4, 4, 2>(p, ksw, st);
   return launch_tiled_cfg<EPI, 2, 2, 2, 2, 4, 2>(p, ksw, st);
 }
 
