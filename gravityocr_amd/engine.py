@@ -266,16 +266,18 @@ class GssEngine:
         K.argmax_accept(logits, target, self.ws_arg, **kw)
 
     # ------------------------------------------------------------------------------------------ prefill ---------
-    def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 48, pos_delta: Optional[torch.Tensor] = None,
+    def prefill(self, slot: int, emb: torch.Tensor, chunk: int = 64, pos_delta: Optional[torch.Tensor] = None,
                 positions: Optional[torch.Tensor] = None, logits_rows: Optional[Tuple[int, int]] = None):
         """Causal prefill of one sequence slot from its prompt embeddings [P, H]. The layer runs the decode
         forward's kernels over all P rows (the tiled GEMM above 64 rows): q|k|v with the RoPE epilogue (or, with
         M-RoPE ``positions``, the plain GEMM and gss_rope_stage_mrope), o_proj and down as k-split parts with the
         parts norms, gate_up with the SwiGLU epilogue; attention runs in causal chunks of ``chunk`` rows through the
-        verify kernel (prefix from the pages, chunk as the window) under the bs = 1 plan, and K/V is committed layer
-        by layer. Every GEMM and norm computes a row the same way at any row count and the attention does not depend
-        on where a key comes from, so a prefilled row equals the AR step of the same token bit for bit. Row j sits
-        at position j (+ pos_delta), or at the M-RoPE positions ``positions`` int32 [P, 3] (t, h, w) when given.
+        verify kernel (prefix from the pages, chunk as the window, at most 64 rows: the widest window the kernels
+        take, and the fastest of 16 / 32 / 48 / 64 for an 8192-token prompt) under the bs = 1 plan, and K/V is
+        committed layer by layer. Every GEMM and norm computes a row the same way at any row count and the attention
+        does not depend on where a key comes from, so a prefilled row equals the AR step of the same token bit for
+        bit (at any chunk size). Row j sits at position j (+ pos_delta), or at the M-RoPE positions ``positions``
+        int32 [P, 3] (t, h, w) when given.
         Returns the logits of the last prompt row [V] (bf16), or of rows [r0, r1) as [r1 - r0, V] when
         ``logits_rows`` = (r0, r1)."""
         c, dev, bf = self.cfg, self.device, torch.bfloat16
