@@ -121,6 +121,20 @@ def test_spec_equals_ar_on_gpu(cuda, cfg_name, bd, n_tok):
     assert spec == ar[:len(spec)]
 
 
+def test_gate_norm_prologue_equals_separate_norm(cuda):
+    """The optional gate_up-prologue norm (fuse_gate_norm, off by default) gives the AR steps' logits bit for bit."""
+    from gravityocr_amd.model import GlmTextConfig
+    cfg = GlmTextConfig(n_layers=4, hidden=1536, n_heads=16, n_kv_heads=2, head_dim=128, ffn=4608, vocab=59392)
+    eng, dec, w, emb = build(cuda, cfg, 2, 500, 16, 16, 1024)
+    assert not eng.fuse_gate_norm
+    toks, logits = gpu_ar(eng, dec, emb, 12)
+    eng.fuse_gate_norm = True
+    toks_f, logits_f = gpu_ar(eng, dec, emb, 12)
+    assert toks_f == toks
+    for a, b in zip(logits, logits_f):
+        assert torch.equal(a, b)
+
+
 def test_kv_committed_by_rounds_equals_ar_kv(cuda):
     from gravityocr_amd.model import TINY
     eng, dec, w, emb = build(cuda, TINY, 3, 256, 16, 4, 1024)
