@@ -8,7 +8,7 @@
 //   consecutive tokens [t * EPT, (t + 1) * EPT)). Softmax of logits / T; the filters keep a prefix of the tokens
 //   in descending probability, so the kept set is {p >= tau} for the smallest tau passing the filter's test,
 //   found by a binary search over the fp32 bit patterns (about 30 block reductions of the count and mass of the tokens
-//   above a candidate); renormalized. Verify mode: row j < K-1 tests its draft token cand[b, j + 1] against its coin
+//   above a candidate; flashinfer's min-p chain runs a second search for top-p above the top-k cut); renormalized. Verify mode: row j < K-1 tests its draft token cand[b, j + 1] against its coin
 //   and draws its residual (the distribution without that token; the last row its full distribution) with the
 //   sequence's uniform; the last of the K workgroups of a sequence resolves the chain (accept length, committed
 //   targets, packed row, next seed). Sample mode (no cand): every row draws from its distribution with its own
@@ -25,7 +25,7 @@ constexpr size_t COUNTER_STRIDE = 32;  // u32 per sequence counter (one 128-byte
 constexpr int SV_MAX_WAVES = 16;
 
 enum { PEN_REPETITION = 1, PEN_PRESENCE = 2, PEN_FREQUENCY = 3, PEN_MIN_NEW_TOKENS = 4 };
-enum { FILTER_NONE = 0, FILTER_JOINT = 1, FILTER_TORCH = 2 };
+enum { FILTER_NONE = 0, FILTER_JOINT = 1, FILTER_TORCH = 2, FILTER_FI_MIN_P = 3 };
 
 struct PenParams {
   float* logits;
@@ -267,25 +267,45 @@ __global__ void __launch_bounds__(NTH) sample_rows_kernel(SvParams p) {
       const float PM = block_max_f<NW>(pmax, redf);
       const int k = p.top_k[b] <= 0 ? 0x7fffffff : p.top_k[b];  // top_k <= 0: no top-k cut
       const float tp = p.top_p[b];
-      // smallest tau (fp32 bit pattern in [0, bits(PM)]) whose strictly-greater count and mass pass the filter;
-      // the test is monotone in tau, so the kept tokens are exactly those with p >= tau
-      uint32_t lo = 0, hi = __float_as_uint(PM);
+      // smallest tau (fp32 bit pattern in [lo, bits(PM)]) whose strictly-greater count C and mass MS pass the
+      // test; the tests are monotone in tau, so the kept tokens are exactly those with p >= tau
+      const uint32_t top = __float_as_uint(PM);
+      auto search = [&](uint32_t lo, auto&& ok) {
+        uint32_t hi = top;
 #pragma unroll 1
-      while (lo < hi) {
-        const uint32_t mid = lo + (hi - lo) / 2;
-        const float tau = __uint_as_float(mid);
-        float c = 0.f, ms = 0.f;
+        while (lo < hi) {
+          const uint32_t mid = lo + (hi - lo) / 2;
+          const float tau = __uint_as_float(mid);
+          float c = 0.f, ms = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPT; ++e)
-          if (pr[e] > tau) { c += 1.f; ms += pr[e]; }
-        const float2 cm = block_sum2<NW>(c, ms, red2);
-        const int C = static_cast<int>(cm.x);
-        const float MS = cm.y;
-        const bool ok = p.mode == FILTER_JOINT ? (C < k && (MS < tp || tp >= 1.f)) : (C < k && !(MS > tp));
-        if (ok) hi = mid; else lo = mid + 1;
+          for (int e = 0; e < EPT; ++e)
+            if (pr[e] > tau) { c += 1.f; ms += pr[e]; }
+          const float2 cm = block_sum2<NW>(c, ms, red2);
+          if (ok(static_cast<int>(cm.x), cm.y)) hi = mid; else lo = mid + 1;
+        }
+        return lo;
+      };
+      float tau;
+      if (p.mode == FILTER_FI_MIN_P) {
+        // top-k renorm, then top-p on the renormalized mass: MS / Z1 < top_p with Z1 the mass the top-k cut keeps
+        uint32_t t = search(0u, [&](int C, float) { return C < k; });
+        if (tp < 1.f) {
+          const float t1 = __uint_as_float(t);
+          float z = 0.f;
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) z += pr[e] >= t1 ? pr[e] : 0.f;
+          const float Z1 = block_sum_f<NW>(z, redf);
+          t = search(t, [&](int, float MS) { return MS / Z1 < tp; });
+        }
+        tau = __uint_as_float(t);
+      } else if (p.mode == FILTER_JOINT) {
+        tau = __uint_as_float(search(0u, [&](int C, float MS) { return C < k && (MS < tp || tp >= 1.f); }));
+      } else {
+        tau = __uint_as_float(search(0u, [&](int C, float MS) { return C < k && !(MS > tp); }));
       }
-      float tau = __uint_as_float(lo);
-      if (p.mode == FILTER_TORCH && p.min_p != nullptr && p.min_p[b] > 0.f) tau = fmaxf(tau, PM * p.min_p[b]);
+      // min-p: p >= min_p * max(p) (the ratio is the same on renormalized probabilities)
+      if ((p.mode == FILTER_TORCH || p.mode == FILTER_FI_MIN_P) && p.min_p != nullptr && p.min_p[b] > 0.f)
+        tau = fmaxf(tau, PM * p.min_p[b]);
       int keep_one = -1;
       if (p.mode == FILTER_TORCH && k == 1) {
         // rank-based top-1: only the lowest-index maximum (the tied maxima are ranked by index)
@@ -453,7 +473,7 @@ extern "C" int gss_sample_rows(const float* logits, int64_t ld_row, int bs, int 
                                void* workspace, size_t workspace_bytes, gss_stream_t stream) {
   if (!logits || !temperature || !uniforms || !sampled || bs <= 0 || K <= 0 || V <= 0 || ld_row < V)
     return GSS_ERR_ARG;
-  if (filter < FILTER_NONE || filter > FILTER_TORCH) return GSS_ERR_ARG;
+  if (filter < FILTER_NONE || filter > FILTER_FI_MIN_P) return GSS_ERR_ARG;
   if (filter != FILTER_NONE && (!top_k || !top_p)) return GSS_ERR_ARG;
   if (cand && !coins) return GSS_ERR_ARG;
   if (K > MAX_K) return GSS_ERR_UNSUPPORTED;

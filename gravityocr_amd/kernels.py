@@ -443,7 +443,7 @@ def gemm_parts(x, w, parts):
 
 
 PENALIZERS = {"repetition": 1, "presence": 2, "frequency": 3, "min_new_tokens": 4}
-FILTERS = {"none": 0, "joint": 1, "torch": 2}
+FILTERS = {"none": 0, "joint": 1, "torch": 2, "flashinfer_min_p": 3}
 
 
 def penalize_rows(logits, cand, state, order):

@@ -16,8 +16,9 @@ walks each grammar along [a0, d_1..] to build the verify rows' packed masks (ful
 selfspec_sampling.py:305-337), and processes the rows in the serving order (selfspec_fast_commit.py:170-194):
 penalties, the grammar mask (gss_apply_vocab_mask), logit_bias, then the custom processor once per row position
 with a read-only request view whose output_ids hold that row's prefix (apply_custom_rows, selfspec_sampling.py:
-200-221). Such rounds synchronize with the host twice and are not captured. Not built: the flashinfer backend's
-min-p path (its top-k / top-p renormalizations are flashinfer's own kernels): it raises.
+200-221). Such rounds synchronize with the host twice and are not captured. The flashinfer backend in a batch that
+needs min_p (any min_p > 0) takes the reference's other branch for every row of the batch (selfspec_sampling.py:
+278-281): top-k renorm, top-p renorm, min-p (gss_sample_rows filter 3).
 """
 from dataclasses import dataclass, field
 from typing import Optional, Sequence
@@ -30,8 +31,9 @@ from .engine import SelfSpecDecoder
 
 @dataclass
 class SamplingSpec:
-    """Per-sequence sampling settings (lists or scalars, broadcast over the batch). ``filter``: "joint" (flashinfer's
-    top-k / top-p, the serving default), "torch" (the pytorch backend, with min_p) or "none". Penalties run in
+    """Per-sequence sampling settings (lists or scalars, broadcast over the batch). ``filter``: "joint" (the flashinfer
+    backend, the serving default: joint top-k / top-p, or its renorm chain with min-p when any min_p > 0), "torch"
+    (the pytorch backend, with min_p) or "none". Penalties run in
     ``order`` (the penalizer orchestrator's order); a penalizer whose parameter is absent is not applied."""
     temperature: object = 1.0
     top_k: object = 0
@@ -123,9 +125,10 @@ class SampledSelfSpec:
         if self.custom is not None and (spec.custom_params is None or len(spec.custom_params) != dec.bs):
             raise ValueError("custom_logit_processor needs one custom_params entry per sequence")
         self.hosted = self.grammars is not None or self.custom is not None
-        if spec.filter == "joint" and _any_positive(spec.min_p):
-            raise NotImplementedError("min_p with the flashinfer backend (its renorm kernels) is not built; "
-                                      "use filter='torch'")
+        if spec.filter not in ("joint", "torch", "none"):
+            raise ValueError(f"filter {spec.filter!r}: 'joint' (flashinfer), 'torch' or 'none'")
+        # the batch-level need_min_p_sampling flag selects the flashinfer backend's renorm chain for every row
+        self.kfilter = "flashinfer_min_p" if spec.filter == "joint" and _any_positive(spec.min_p) else spec.filter
         self.dec, self.spec = dec, spec
         e, bs, Kw, V = dec.eng, dec.bs, dec.st.K, dec.eng.cfg.vocab
         dev = e.device
@@ -213,7 +216,7 @@ class SampledSelfSpec:
                 logits[rows] = self.custom(logits[rows], params)
 
     def _draw(self, logits, bs, Kr, uniforms, out):
-        K.sample_rows(logits, bs, Kr, temperature=self.temperature, filter=self.spec.filter, top_k=self.top_k,
+        K.sample_rows(logits, bs, Kr, temperature=self.temperature, filter=self.kfilter, top_k=self.top_k,
                       top_p=self.top_p, min_p=self.min_p, uniforms=uniforms, sampled=out)
 
     def _cumulate(self, tok, valid):
@@ -261,7 +264,7 @@ class SampledSelfSpec:
         self.u.uniform_()
         if keep:
             self.keep = (rows.clone(), self.coins.clone(), self.u.clone(), s.am.clone())
-        K.sample_rows(rows, bs, Kw, temperature=self.temperature, filter=self.spec.filter, top_k=self.top_k,
+        K.sample_rows(rows, bs, Kw, temperature=self.temperature, filter=self.kfilter, top_k=self.top_k,
                       top_p=self.top_p, min_p=self.min_p, cand=s.am, coins=self.coins, uniforms=self.u,
                       sampled=self.sampled, target=s.tgt, accept_len=s.acc, next_x0=s.x0, packed=s.packed,
                       workspace=self.ws)
@@ -302,7 +305,7 @@ class SampledSelfSpec:
         self.u.uniform_()
         if keep:
             self.keep = (rows.clone(), self.coins.clone(), self.u.clone(), s.am.clone())
-        K.sample_rows(rows, bs, Kw, temperature=self.temperature, filter=self.spec.filter, top_k=self.top_k,
+        K.sample_rows(rows, bs, Kw, temperature=self.temperature, filter=self.kfilter, top_k=self.top_k,
                       top_p=self.top_p, min_p=self.min_p, cand=s.am, coins=self.coins, uniforms=self.u,
                       sampled=self.sampled, target=s.tgt, accept_len=s.acc, next_x0=s.x0, packed=s.packed,
                       workspace=self.ws)

@@ -223,7 +223,10 @@ int gss_apply_vocab_mask(float* logits, int64_t ld_row, int rows, int V, const i
  * joint top-k / top-p: token q kept iff #{p > p_q} < top_k[b] and sum{p > p_q} < top_p[b], top_p >= 1 keeping
  * all; selfspec_sampling.py:230-244) or 2 (the pytorch backend: rank < top_k, mass before <= top_p, p >= max(p) *
  * min_p[b]; selfspec_sampling.py:253-263; tied values are kept or dropped together except the top-1 cut, which keeps
- * the lowest index), renormalized; top_k <= 0 means no top-k cut. A draw with uniform u is the smallest token whose
+ * the lowest index) or 3 (the flashinfer backend in a batch that needs min_p, selfspec_sampling.py:276-281: tokens
+ * with #{p > p_q} < top_k[b], renormalized; of those, tokens whose strictly greater renormalized mass is below
+ * top_p[b] (top_p >= 1 keeps all); then p >= max(p) * min_p[b] when min_p is given and min_p[b] > 0),
+ * renormalized; top_k <= 0 means no top-k cut. A draw with uniform u is the smallest token whose
  * prefix sum (index order) exceeds u * total.
  * Sample mode (cand NULL): sampled[b, r] = a draw from row (b, r) with uniforms[b * K + r] (a0 from the draft's
  * causal row: K = 1, ld_row = the stride between the sequences' rows).

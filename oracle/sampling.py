@@ -111,15 +111,35 @@ def torch_backend_filter(p: np.ndarray, k: int, top_p: float, min_p: float, need
     return q / q.sum()
 
 
+def flashinfer_min_p_chain(p: np.ndarray, k: int, top_p: float, min_p: float) -> np.ndarray:
+    """S:278-281 (the flashinfer backend when the batch needs min_p): top_k_renorm_probs, then top_p_renorm_probs on
+    the renormalized result, then S:247-251's min-p cut (p >= min_p * max(p)), renormalizing after each step.
+
+    top_k_renorm_probs and top_p_renorm_probs are flashinfer's (flashinfer-python, not vendored; the reference's
+    sglang patch binds them through sglang.srt.layers.sampler). Their published behaviour, restated here: top-k keeps
+    the tokens with fewer than k strictly greater probabilities, top-p keeps those whose strictly greater mass is below
+    top_p (top_p >= 1 keeps every token). How flashinfer's pivot search treats tied probabilities at the cut, and its
+    float32 rounding of the renormalized mass, are not restated: parity unpinned for ties and for rows whose mass sits
+    within float32 rounding of top_p."""
+    q = joint_top_k_top_p(p, k, 1.0)
+    q = joint_top_k_top_p(q, q.shape[0] + 1, top_p)
+    keep = q >= q.max() * min_p
+    q = np.where(keep, q, 0.0)
+    return q / q.sum()
+
+
 def target_probs(logits_row: np.ndarray, temperature: float, mode: int, k: int, top_p: float,
                  min_p: float = 0.0) -> np.ndarray:
-    """S:266-286 for one row: mode 0 = no filter (softmax only), 1 = flashinfer joint top-k/top-p (no min_p), 2 = the
-    pytorch backend (min_p applied when > 0)."""
+    """S:266-286 for one row: mode 0 = no filter (softmax only), 1 = flashinfer joint top-k/top-p (a batch without
+    min_p), 2 = the pytorch backend (min_p applied when > 0), 3 = the flashinfer backend in a batch that needs min_p
+    (top-k renorm, top-p renorm, min-p; a row whose own min_p is 0 still takes the two renorm steps)."""
     p = softmax_t(logits_row, temperature)
     if mode == 0:
         return p
     if mode == 1:
         return joint_top_k_top_p(p, k, top_p)
+    if mode == 3:
+        return flashinfer_min_p_chain(p, k, top_p, min_p)
     return torch_backend_filter(p, k, top_p, min_p, min_p > 0.0)
 
 

@@ -61,14 +61,16 @@ def test_top1_sampled_round_equals_sampled_ar(cuda, pen):
     assert int(dec.accept_lengths(rounds).sum()) > 0
 
 
-@pytest.mark.parametrize("filt,pen", [("joint", {}), ("torch", PEN)], ids=["joint", "torch-penalties"])
-def test_sampled_round_decisions_match_oracle(cuda, filt, pen):
+@pytest.mark.parametrize("filt,min_p,mode,pen", [("joint", 0.0, 1, {}), ("torch", 0.05, 2, PEN), ("joint", 0.05, 3, {})],
+                         ids=["joint", "torch-penalties", "joint-min_p"])
+def test_sampled_round_decisions_match_oracle(cuda, filt, min_p, mode, pen):
+    """mode = the oracle's target distribution: the flashinfer backend with min_p > 0 in the batch is its renorm
+    chain (top-k renorm, top-p renorm, min-p)."""
     from gravityocr_amd.sampling import SampledSelfSpec, SamplingSpec
-    print(f"sampled decisions {filt}", flush=True)
+    print(f"sampled decisions {filt} min_p={min_p}", flush=True)
     torch.manual_seed(3)
     eng, dec, emb = _build(cuda)
-    spec = SamplingSpec(temperature=0.8, top_k=40, top_p=0.9, min_p=0.05 if filt == "torch" else 0.0, filter=filt,
-                        **pen)
+    spec = SamplingSpec(temperature=0.8, top_k=40, top_p=0.9, min_p=min_p, filter=filt, **pen)
     ss = SampledSelfSpec(dec, spec)
     last = eng.prefill(0, emb)
     ss.start(last.float().argmax().view(1))
@@ -78,7 +80,7 @@ def test_sampled_round_decisions_match_oracle(cuda, filt, pen):
         ss.round(keep=True)
         torch.cuda.synchronize()
         rows, coins, u, cand = (t.cpu().numpy() for t in ss.keep)
-        probs = np.stack([S.target_probs(rows[j], 0.8, 1 if filt == "joint" else 2, 40, 0.9, spec.min_p)
+        probs = np.stack([S.target_probs(rows[j], 0.8, mode, 40, 0.9, spec.min_p)
                           for j in range(K)])
         a_want, tok_want, t_want = S.spec_sample_chain(probs, cand[0], coins[0].astype(np.float64), float(u[0]))
         a = int(dec.st.acc[0])

@@ -71,7 +71,8 @@ CASES = [  # (filter, temperature, top_k, top_p, min_p)
     ("none", 1.0, 0, 1.0, 0.0), ("none", 0.7, 0, 1.0, 0.0), ("none", 0.0, 0, 1.0, 0.0),
     ("joint", 1.0, 20, 0.9, 0.0), ("joint", 0.8, 1, 1.0, 0.0), ("joint", 1.3, 0, 0.5, 0.0), ("joint", 1.0, 5, 1.0, 0.0),
     ("torch", 1.0, 50, 0.95, 0.0), ("torch", 0.9, 1, 1.0, 0.0), ("torch", 1.0, 0, 0.8, 0.05),
-    ("torch", 1.2, 30, 1.0, 0.1)]
+    ("torch", 1.2, 30, 1.0, 0.1), ("flashinfer_min_p", 1.0, 20, 0.9, 0.1), ("flashinfer_min_p", 0.8, 0, 0.7, 0.0),
+    ("flashinfer_min_p", 1.2, 40, 1.0, 0.3), ("flashinfer_min_p", 1.0, 60, 0.5, 0.02)]
 
 
 def _target(row, case):
@@ -80,7 +81,7 @@ def _target(row, case):
         q = np.zeros(row.shape[0])
         q[int(np.argmax(row))] = 1.0
         return q
-    mode = {"none": 0, "joint": 1, "torch": 2}[filt]
+    mode = {"none": 0, "joint": 1, "torch": 2, "flashinfer_min_p": 3}[filt]
     return S.target_probs(row, T, mode, k if k > 0 else row.shape[0] + 1, tp, mp)
 
 
@@ -107,7 +108,8 @@ def test_sample_mode_draws_match_oracle(cuda, V, case):
 
 
 @pytest.mark.parametrize("V", [4096, 59392])
-@pytest.mark.parametrize("case", [CASES[0], CASES[3], CASES[7], CASES[9], CASES[2]], ids=lambda c: "-".join(map(str, c)))
+@pytest.mark.parametrize("case", [CASES[0], CASES[3], CASES[7], CASES[9], CASES[2], CASES[11], CASES[14]],
+                         ids=lambda c: "-".join(map(str, c)))
 def test_verify_mode_chain_matches_oracle(cuda, V, case):
     """Speculative sampling of a draft chain: drafts are high-probability tokens of the rows (so several are
     accepted), coins spread over (0, 1]; every sequence's accept length, targets, next seed and packed row equal the

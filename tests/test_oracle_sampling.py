@@ -44,6 +44,59 @@ def test_filters_match_definitions(seed):
                                                brute_torch(p, k, top_p, min_p), rtol=0, atol=1e-12)
 
 
+def brute_fi_min_p(p, k, top_p, min_p):
+    """The three flashinfer steps one token at a time, each on the previous step's renormalized vector."""
+    def renorm(keep, x):
+        y = np.array([x[i] if keep[i] else 0.0 for i in range(len(x))])
+        return y / y.sum()
+    q = renorm([sum(1 for v in p if v > p[i]) < k for i in range(len(p))], p)
+    q = renorm([top_p >= 1.0 or sum(v for v in q if v > q[i]) < top_p for i in range(len(q))], q)
+    return renorm([q[i] >= max(q) * min_p for i in range(len(q))], q)
+
+
+def test_flashinfer_min_p_chain_known_answers():
+    """Hand-worked rows. [0.4, 0.3, 0.2, 0.1], k = 2, top_p = 0.5: top-k leaves [4/7, 3/7]; the second token has 4/7
+    above it, so top-p keeps only the first (the joint filter, which tests top-p on the unrenormalized mass 0.4, keeps
+    both). [0.5, 0.3, 0.15, 0.05], k = 3, top_p = 0.9, min_p = 0.4: top-k renorm [10/19, 6/19, 3/19]; top-p keeps
+    all three (16/19 < 0.9); min-p drops 3/19 < 0.4 * 10/19, leaving [5/8, 3/8]."""
+    np.testing.assert_allclose(S.flashinfer_min_p_chain(np.array([0.4, 0.3, 0.2, 0.1]), 2, 0.5, 0.0),
+                               [1.0, 0.0, 0.0, 0.0], rtol=0, atol=1e-15)
+    np.testing.assert_allclose(S.joint_top_k_top_p(np.array([0.4, 0.3, 0.2, 0.1]), 2, 0.5),
+                               [4 / 7, 3 / 7, 0.0, 0.0], rtol=0, atol=1e-15)
+    np.testing.assert_allclose(S.flashinfer_min_p_chain(np.array([0.5, 0.3, 0.15, 0.05]), 3, 0.9, 0.4),
+                               [0.625, 0.375, 0.0, 0.0], rtol=0, atol=1e-15)
+    # min_p = 0 with neutral top-k / top-p: the untouched distribution
+    p = np.array([0.25, 0.5, 0.125, 0.125])
+    np.testing.assert_array_equal(S.flashinfer_min_p_chain(p, 5, 1.0, 0.0), p)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_flashinfer_min_p_chain_definitions_and_reductions(seed):
+    """Brute force (ties included), and the special cases that reduce to filters pinned above: no top-k / top-p ->
+    the pytorch backend's min-p alone; min_p = 0 and top_p = 1 -> the joint filter's top-k; min_p = 0 and no top-k ->
+    the joint filter's top-p."""
+    g = np.random.default_rng(100 + seed)
+    V = 32
+    logits = g.normal(size=V) * 2
+    logits[g.integers(0, V, 5)] = logits[7]
+    for T in (0.6, 1.0, 1.5):
+        p = S.softmax_t(logits, T)
+        for k in (1, 4, 9, V):
+            for top_p in (0.3, 0.8, 1.0):
+                for min_p in (0.0, 0.1, 0.5):
+                    np.testing.assert_allclose(S.flashinfer_min_p_chain(p, k, top_p, min_p),
+                                               brute_fi_min_p(p, k, top_p, min_p), rtol=0, atol=1e-12)
+        for min_p in (0.02, 0.2, 0.7):
+            np.testing.assert_allclose(S.flashinfer_min_p_chain(p, V + 1, 1.0, min_p),
+                                       S.torch_backend_filter(p, V + 1, 1.0, min_p, True), rtol=0, atol=1e-12)
+        for k in (1, 3, 10):
+            np.testing.assert_allclose(S.flashinfer_min_p_chain(p, k, 1.0, 0.0), S.joint_top_k_top_p(p, k, 1.0),
+                                       rtol=0, atol=1e-12)
+        for top_p in (0.2, 0.6, 0.95):
+            np.testing.assert_allclose(S.flashinfer_min_p_chain(p, V + 1, top_p, 0.0),
+                                       S.joint_top_k_top_p(p, V + 1, top_p), rtol=0, atol=1e-12)
+
+
 def test_greedy_request_is_a_point_mass():
     """SGLang turns a greedy request into top_k = 1: both filters then keep only the maximum."""
     p = S.softmax_t(np.array([0.1, 2.0, -1.0, 1.5]), 1.0)
