@@ -125,9 +125,18 @@ GSS_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // see an LDS store in flight: it would otherwise wait for every outstanding one (vmcnt(0)) before the next LDS read,
 // including the loads of a stage being prefetched while the current one is computed. The kernels order these loads
 // themselves: s_waitcnt vmcnt on the issuing wave, then a workgroup barrier, before any wave reads the data.
-GSS_DEV void dma16(const void* g, const void* lds) {
-  const uint32_t la = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(la) : "memory");
+// The same load from a wave-uniform base held in scalar registers plus a 32-bit per-lane byte offset, into the LDS
+// byte address lds (wave-uniform): no 64-bit address arithmetic per lane.
+GSS_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+
+// A pointer that is the same in every lane, moved to scalar registers (no-op when it already is there).
+GSS_DEV const char* uniform_ptr(const void* p) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // Boundary tiles ts..te-1 of a stage held in LDS (tile t's K at lds_k + (t - ts) * TILE * D, V likewise), t0 the
@@ -298,33 +307,44 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
     }
   };
 
-  // ---- tile loads, global -> LDS directly (dma16: lane i of an instruction writes the 16 bytes at the
+  // ---- tile loads, global -> LDS directly (dma16s: lane i of an instruction writes the 16 bytes at the
   // instruction's LDS base + 16 i) into a ring of NSLOT one-tile slots, each K [TILE][D] (XOR-swizzled 16-byte
-  // chunks) then V [4 pages][D][16]. Every instruction covers 64 chunks of one (page, head) block, so its page id is
-  // wave-uniform. Loads are unconditional: pages past the prefix read page 0 (in bounds) and the boundary fix
-  // overwrites those positions.
+  // chunks) then V [4 pages][D][16]. Instruction ib of the K (or V) tile covers the 64 chunks of pattern
+  // pat = ib % PAGE_INSTR of page ib / PAGE_INSTR, so its page id is wave-uniform. A wave issues one instruction
+  // every few clocks at best, so the issue code is kept to scalar work plus at most two VALU operations per load: the
+  // per-lane byte offsets of pattern 0 are computed once; pattern pat adds pat * 1024 bytes (in the scalar base) and,
+  // for K, XORs (pat * 64 / CH) % CH into the lane's swizzled chunk index. Loads are unconditional: pages past the
+  // prefix read page 0 (in bounds) and the boundary fix overwrites those positions after the loads have landed.
   constexpr int NSLOT = LY::NSLOT;
-  auto issue_tile = [&](int i) {  // tile t_beg + i of the split -> slot i % NSLOT
-    uint16_t* buf = smem + (i % NSLOT) * LY::SLOT_EL;
+  constexpr int N_INSTR = 2 * TILE_INSTR;                // K then V instructions of a tile
+  constexpr int PER_WAVE = (N_INSTR + NW - 1) / NW;      // this wave's: wv, wv + NW, ...
+  const uint32_t ktok0 = lane / CH;                      // the lane's token within a K pattern
+  const uint32_t kc0 = (lane % CH) ^ (ktok0 & (CH - 1));  // its swizzled chunk index, pattern 0
+  const uint32_t k_lane = ktok0 * D * 2;
+  const uint32_t v_lane = ((lane >> 1) * PAGE + ((lane & 1) ^ ((lane >> 4) & 1)) * 8) * 2;  // (d, half) chunk
+  const char* k_base = uniform_ptr(kp_head);
+  const char* v_base = uniform_ptr(vp_head);
+  const uint32_t page_bytes = static_cast<uint32_t>(page_stride * 2);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)));
+  auto issue_tile = [&](int i) __attribute__((always_inline)) {  // tile t_beg + i -> slot i % NSLOT
+    const uint32_t slot = lds0 + (i % NSLOT) * (LY::SLOT_EL * 2);
     const int pgv = lane < TILE / PAGE ? spages[i * (TILE / PAGE) + lane] : 0;
-#pragma unroll 1  // unrolled, the per-instruction lane offsets are hoisted out of the tile loop and spilled
-    for (int k = 0; k < (2 * TILE_INSTR + NW - 1) / NW; ++k) {
-      const int ii = wv + k * NW;
-      if (ii >= 2 * TILE_INSTR) break;
+    // the per-instruction scalars are a few operations from wv; kept opaque here so the compiler recomputes them
+    // per tile instead of holding a register for each across the tile loop
+    uint32_t w = static_cast<uint32_t>(wv);
+    asm volatile("" : "+s"(w));
+    __builtin_assume(w < NW);
+#pragma unroll
+    for (uint32_t k = 0; k < PER_WAVE; ++k) {
+      const uint32_t ii = w + k * NW;
+      if (PER_WAVE * NW != N_INSTR && ii >= N_INSTR) break;  // wave-uniform; only when NW does not divide it
       const bool is_v = ii >= TILE_INSTR;
-      const int ib = is_v ? ii - TILE_INSTR : ii;
-      const int pblk = ib / PAGE_INSTR, pat = ib % PAGE_INSTR;
-      const int kr = pat * 64 + lane;
-      int off;  // element offset in the (page, head) block
-      if (is_v) {
-        const int vd = kr >> 1, vh = (kr & 1) ^ ((vd >> 3) & 1);
-        off = vd * PAGE + vh * 8;
-      } else {
-        const int ktok = kr / CH;
-        off = ktok * D + ((kr % CH) ^ (ktok & (CH - 1))) * 8;
-      }
-      const int64_t page = __builtin_amdgcn_readlane(pgv, pblk);
-      dma16((is_v ? vp_head : kp_head) + page * page_stride + off, buf + (is_v ? TILE_EL : 0) + ib * 512);
+      const uint32_t ib = is_v ? ii - TILE_INSTR : ii;
+      const uint32_t pblk = ib / PAGE_INSTR, pat = ib % PAGE_INSTR;
+      const uint32_t page = __builtin_amdgcn_readlane(pgv, pblk);
+      const char* sb = (is_v ? v_base : k_base) + (static_cast<uint64_t>(page) * page_bytes + pat * 1024);
+      const uint32_t xr = (pat * (64 / CH)) & (CH - 1);
+      dma16s(sb, is_v ? v_lane : k_lane + ((kc0 ^ xr) << 4), slot + (is_v ? TILE_EL * 2 : 0) + ib * 1024);
     }
   };
   // Tile i reaching past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
@@ -610,22 +630,36 @@ __global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams
     const int pos = (t_beg + st * RG_LANES) * TILE + lane * PAGE;
     return (lane < RG_LANES * (TILE / PAGE) && pos < L) ? pt[pos / PAGE] : 0;
   };
-  auto issue_stage = [&](int st, int pgv) {
-#pragma unroll 4
-    for (int i = 0; i < 2 * STAGE_INSTR / NW; ++i) {
-      const int ii = i * NW + wv;
+  // A wave issues one instruction every few clocks at best, so each load is a handful of scalar operations on
+  // wave-uniform values (the page base in scalar registers, the lane's byte offset computed once above).
+  const uint32_t koff_b = koff * 2, voff_b = voff * 2;
+  const char* k_base = uniform_ptr(p.k_pages + kvh * head_stride);
+  const char* v_base = uniform_ptr(p.v_pages + kvh * head_stride);
+  const uint32_t page_bytes = static_cast<uint32_t>(p.Hkv * head_stride * 2);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(smem)));
+  auto issue_stage = [&](int st, int pgv) __attribute__((always_inline)) {
+    // the page ids (and the queries) have landed before the first load is issued: the compiler does not count the
+    // direct-to-LDS loads, so a wait it placed for pgv between them would also wait for every load issued before it
+    __builtin_amdgcn_s_waitcnt(0);
+    // the per-instruction scalars are a few operations from wv; kept opaque so they are not held across stages
+    uint32_t w = static_cast<uint32_t>(wv);
+    asm volatile("" : "+s"(w));
+    __builtin_assume(w < NW);
+#pragma unroll
+    for (uint32_t i = 0; i < 2 * STAGE_INSTR / NW; ++i) {
+      const uint32_t ii = i * NW + w;
       const bool is_v = ii >= STAGE_INSTR;
-      const int iv = is_v ? ii - STAGE_INSTR : ii;
-      const int t = t_beg + st * RG_LANES + iv / TILE_INSTR;
+      const uint32_t iv = is_v ? ii - STAGE_INSTR : ii;
+      const int t = t_beg + st * RG_LANES + static_cast<int>(iv / TILE_INSTR);
       if (t >= t_end) continue;
-      const int pblk = iv / PAGE_INSTR;                         // page of the stage (tile * 4 + page in tile)
-      const int pos0 = t * TILE + (pblk % (TILE / PAGE)) * PAGE;  // first position of that page
-      const int64_t page = __builtin_amdgcn_readlane(pgv, pblk);
-      const uint16_t* base = (is_v ? p.v_pages : p.k_pages) + (page * p.Hkv + kvh) * head_stride;
-      const bool in_prefix = pos0 + PAGE <= L || (is_v ? pos0 + vh * 8 < L : pos0 + ktok < L);
-      if (in_prefix)
-        __builtin_amdgcn_global_load_lds((gvoid_t*)(base + (is_v ? voff : koff)),
-                                         (lvoid_t*)(smem + (is_v ? LdsRG<D>::V_OFF : 0) + iv * 512), 16, 0, 0);
+      const uint32_t pblk = iv / PAGE_INSTR;                                 // page of the stage (tile * 4 + page)
+      const int pos0 = t * TILE + static_cast<int>(pblk % (TILE / PAGE)) * PAGE;  // first position of that page
+      const uint32_t page = __builtin_amdgcn_readlane(pgv, pblk);
+      const char* sb = (is_v ? v_base : k_base) + static_cast<uint64_t>(page) * page_bytes;
+      const uint32_t lds = lds0 + (is_v ? LdsRG<D>::V_OFF * 2 : 0) + iv * 1024;
+      // chunks of positions >= L are not loaded (the lane's first position in the page is below PAGE, so this one
+      // compare also keeps every chunk of a page that lies inside the prefix)
+      if (pos0 + (is_v ? vh * 8 : ktok) < L) dma16s(sb, is_v ? voff_b : koff_b, lds);
     }
   };
   // Tiles that reach past the prefix: K rows and V columns of positions >= L get the window rows (staging) or zero,
