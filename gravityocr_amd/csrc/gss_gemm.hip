@@ -87,6 +87,20 @@ typedef __attribute__((address_space(3))) void lvoid_t;  // LDS (its destination
 // rows of one fragment read land in 16 different bank groups.
 GSS_DEV int xs_slot(int r, int c, int cpr) { return r * cpr + (c ^ (r & 15)); }
 
+// global -> LDS, 16 bytes per lane, from a wave-uniform base held in scalar registers plus a 32-bit per-lane byte
+// offset, into the wave-uniform LDS byte address lds + 16 * lane: no 64-bit address arithmetic per lane
+GSS_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+}
+
+// a pointer that is the same in every lane, moved to scalar registers (no-op when it already is there)
+GSS_DEV const char* uniform_ptr(const void* ptr) {
+  const uint64_t a = reinterpret_cast<uint64_t>(ptr);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  return reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector memory operations are outstanding and
 // leaves the other counters free: vmcnt[3:0] in bits 3:0, expcnt 7 in bits 6:4, lgkmcnt 15 in bits 11:8. The
 // builtin form lets the compiler's own wait counting see the direct-to-LDS loads complete.
@@ -382,19 +396,29 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   };
 
   uint16_t* xs = reinterpret_cast<uint16_t*>(red + NW * FT * NT * 64);
-  const int cpr = ksw * 4;
+  // XS runs only with ksw == UNR (the host checks), so a staged row holds a compile-time 4 * UNR chunks
+  const int cpr = XS ? UNR * 4 : ksw * 4;
   uint16_t* xw = xs + wv * Ms * cpr * 8;  // XS: this wave's staged rows
   if constexpr (XS) {
-    // one pass (ksw <= UNR): rows 0..Ms-1, k-steps [s_beg, s_end) -> LDS, issued before the weight loads below
-    const int n_slots = Ms * cpr, live_chunks = (s_end - s_beg) * 4;
-    const uint16_t* xbase = xs0 + static_cast<int64_t>(s_beg) * 32;
+    // one pass: rows 0..Ms-1, k-steps [s_beg, s_end) -> LDS, issued before the weight loads below. LDS slot
+    // q = j * 64 + lane holds chunk (q % CPR) ^ (r & 15) of row r = q / CPR; each instruction is a few VALU
+    // operations on a row offset that steps by a uniform amount (a wave issues one instruction every few clocks, and
+    // these loads go out before the weights').
+    constexpr int CPR = UNR * 4, DR = 64 / CPR;
+    static_assert(64 % CPR == 0 && CPR >= 16, "a chunk swizzle by r & 15 must stay inside the row");
+    const int n_slots = Ms * CPR, live_chunks = (s_end - s_beg) * 4;
+    const char* xbase = uniform_ptr(xs0 + static_cast<int64_t>(s_beg) * 32);
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(xw)));
+    const int cl = lane % CPR;
+    int r = lane / CPR;
+    uint32_t rofs = static_cast<uint32_t>(r * p.ldx * 2);
+    const uint32_t rstep = static_cast<uint32_t>(DR * p.ldx * 2);
 #pragma unroll 1
     for (int j = 0; j * 64 < n_slots; ++j) {
-      const int q = j * 64 + lane;
-      const int r = q / cpr, c = (q % cpr) ^ (r & 15);
-      if (q < n_slots && c < live_chunks)
-        __builtin_amdgcn_global_load_lds((gvoid_t*)(xbase + static_cast<int64_t>(r) * p.ldx + c * 8),
-                                         (lvoid_t*)(xw + j * 512), 16, 0, 0);
+      const int c = cl ^ (r & 15);
+      if (j * 64 + lane < n_slots && c < live_chunks) dma16s(xbase, rofs + c * 16, lds0 + j * 1024);
+      r += DR;
+      rofs += rstep;
     }
   }
   // PRO_ADDNORM runs exactly one pass on every wave (the prologue has a workgroup barrier)
@@ -1109,7 +1133,8 @@ int launch_ft_nt(GemmParams& p, void* ws, size_t ws_bytes, hipStream_t st) {
     }
     // activations staged in LDS when a wave's k-range is one pass and the rows fit (same arithmetic either way)
     const size_t lds_xs = lds + static_cast<size_t>(nw) * Mw * ksw * 64;
-    const bool xs = kStageX && lds_xs <= MAX_DYN_LDS;
+    // (the staged rows are addressed by 32-bit byte offsets from the first)
+    const bool xs = kStageX && lds_xs <= MAX_DYN_LDS && static_cast<int64_t>(p.M) * p.ldx * 2 < (int64_t{1} << 31);
     if constexpr (FT + NT <= 3) {
       if (ksw % 8 == 0) {
         constexpr auto kx = gemm_kernel<FT, NT, 8, EPI, PRO_NONE, 8, POST, true>;
