@@ -234,15 +234,15 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
   if (v >= p.n_units) return;  // padding of the last group of 8 units
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  __shared__ int s_unit[3];  // (sequence, kv head, split) of unit v; sequence -1: v is past the valid units
+  __shared__ int s_unit[4];  // (sequence, kv head, split, prefix length) of unit v; sequence -1: past the valid units
   if (wv == 0) {
     int base = 0;  // valid units of the sequences before this 64-sequence chunk
-    int found = -1, fh = 0, fs = 0;
+    int found = -1, fh = 0, fs = 0, fl = 0;
     for (int c = 0; c < p.bs && found < 0 && base <= v; c += 64) {
       const int bb = c + lane;
-      int nvb = 0;  // valid splits of sequence bb
+      int nvb = 0, Lb = 0;  // valid splits and committed prefix length of sequence bb
       if (bb < p.bs) {
-        const int Lb = min(max(p.prefix_len[bb] + p.prefix_extra, 0), p.cap);
+        Lb = min(max(p.prefix_len[bb] + p.prefix_extra, 0), p.cap);
         nvb = min(p.n_split, valid_splits(Lb, p.W, p.tps));
       }
       int inc = nvb * p.Hkv;  // inclusive prefix sum of the chunk's unit counts
@@ -257,6 +257,7 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
       if (bal) {
         const int src = __builtin_ctzll(bal);
         const int r = __shfl(v - lo, src, 64), nv = __shfl(nvb, src, 64);
+        fl = __shfl(Lb, src, 64);
         found = c + src;
         fh = r / nv;
         fs = r % nv;
@@ -267,6 +268,7 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
       s_unit[0] = found;
       s_unit[1] = fh;
       s_unit[2] = fs;
+      s_unit[3] = fl;
     }
   }
   __syncthreads();
@@ -276,9 +278,9 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
   if (b < 0) return;  // past the last valid unit
   const int rw = wv;  // row wave
   const int l16 = lane & 15, g4 = lane >> 4;
-  // committed prefix length; clamped to the plan's capacity and to what the page-table row can address, so every
-  // key falls in one of the plan's splits and every page-table read is in bounds
-  const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.cap);
+  // committed prefix length (from the scan above); clamped to the plan's capacity and to what the page-table row
+  // can address, so every key falls in one of the plan's splits and every page-table read is in bounds
+  const int L = __builtin_amdgcn_readfirstlane(s_unit[3]);
   const int W = p.W, nc = p.n_causal;
   const int n_tiles = (L + W + TILE - 1) / TILE;
   const int t_beg = s * p.tps, t_end = min(n_tiles, t_beg + p.tps);
