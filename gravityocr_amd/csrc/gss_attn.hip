@@ -124,9 +124,9 @@ GSS_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // `lds` + 16 i; `lds` is wave-uniform and goes through M0). Written as inline assembly so that the compiler does not
 // see an LDS store in flight: it would otherwise wait for every outstanding one (vmcnt(0)) before the next LDS read,
 // including the loads of a stage being prefetched while the current one is computed. The kernels order these loads
-// themselves: s_waitcnt vmcnt on the issuing wave, then a workgroup barrier, before any wave reads the data.
-// The same load from a wave-uniform base held in scalar registers plus a 32-bit per-lane byte offset, into the LDS
-// byte address lds (wave-uniform): no 64-bit address arithmetic per lane.
+// themselves: s_waitcnt vmcnt on the issuing wave, then a workgroup barrier, before any wave reads the data. The
+// source is a wave-uniform base held in scalar registers plus a 32-bit per-lane byte offset: no 64-bit address
+// arithmetic per lane.
 GSS_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
