@@ -1,8 +1,9 @@
 // (c) Fused LM-head argmax + accept-longest-prefix + bonus token, in one launch.
 //
-// Phase 1: workgroup (chunk, row) scans 4096 logits of one row (16 per thread, 16-byte loads), keeps the best
-//   (value, index) under the greedy rule (max value, lowest index on ties, NaN as max), reduces across the
-//   wavefront with xor-shuffles and across the workgroup through LDS, and stores the chunk's winner.
+// Phase 1: workgroup (chunk, row) scans 1, 2 or 4 pieces of 4096 logits of one row (16 per thread per piece,
+//   16-byte loads; more pieces per workgroup for larger batches), keeps the best (value, index) under the greedy
+//   rule (max value, lowest index on ties, NaN as max), reduces across the wavefront with xor-shuffles and across
+//   the workgroup through LDS, and stores the chunk's winner.
 // Phase 2: the last workgroup to finish for a sequence (chunk winners handed over through the coherence point and
 //   two levels of atomic counters in the workspace) reduces the chunk winners of each of its W rows in chunk order, then runs the linear-chain accept:
 //   acc = leading r with target[r] == window[r+1]; next_x0 = target[acc]; packed row as the reference's readback.
@@ -64,7 +65,8 @@ GSS_DEV int load16(const T* row, int j0, int V, float (&vals)[PER_THREAD]) {
     return PER_THREAD;
   }
   const int n = V - j0 < PER_THREAD ? V - j0 : PER_THREAD;
-  for (int e = 0; e < n; ++e) vals[e] = load_logit<T>(row, j0 + e);
+#pragma unroll
+  for (int e = 0; e < PER_THREAD; ++e) vals[e] = e < n ? load_logit<T>(row, j0 + e) : -INFINITY;  // static indices
   return n;
 }
 
@@ -121,7 +123,10 @@ struct ArgParams {
 };
 
 
-template <typename T>
+// SPC: CHUNK-logit pieces of the row per workgroup (chunk c covers pieces [c * SPC, (c + 1) * SPC)); the winner is
+// the maximum of a strict total order, so it does not depend on how the row is cut. A thread loads all its pieces
+// before comparing, so they are in flight together.
+template <typename T, int SPC>
 __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p) {
   const int chunk = blockIdx.x, row = blockIdx.y;  // row = b * W + r
   const int b = row / p.W;
@@ -130,8 +135,31 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
 
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  const int j0 = chunk * CHUNK + tid * PER_THREAD;
-  if (j0 < p.V) scan16<T>(lrow, j0, p.V, bv, bi);
+  if constexpr (SPC == 1) {
+    const int j0 = chunk * CHUNK + tid * PER_THREAD;
+    if (j0 < p.V) scan16<T>(lrow, j0, p.V, bv, bi);
+  } else {
+    float vals[SPC][PER_THREAD];
+    int n[SPC];
+#pragma unroll
+    for (int q = 0; q < SPC; ++q) {
+      const int j0 = (chunk * SPC + q) * CHUNK + tid * PER_THREAD;
+      n[q] = j0 < p.V ? load16<T>(lrow, j0, p.V, vals[q]) : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < SPC; ++q) {  // pieces in index order, each in index order
+      const int j0 = (chunk * SPC + q) * CHUNK + tid * PER_THREAD;
+      if (n[q] == PER_THREAD) {
+#pragma unroll
+        for (int e = 0; e < PER_THREAD; ++e)
+          if (beats(vals[q][e], j0 + e, bv, bi)) { bv = vals[q][e]; bi = j0 + e; }
+      } else {
+#pragma unroll
+        for (int e = 0; e < PER_THREAD; ++e)
+          if (e < n[q] && beats(vals[q][e], j0 + e, bv, bi)) { bv = vals[q][e]; bi = j0 + e; }
+      }
+    }
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float ov = __shfl_xor(bv, o, 64);
@@ -218,6 +246,33 @@ size_t ws_bytes(int bs, int W, int V) {
 
 }  // namespace
 
+// Pieces per workgroup: as many as keep about four workgroups per CU (one piece per workgroup for a single
+// sequence's 17 rows, whose 255 workgroups already fill the chip once), at most 4.
+static int pieces_per_chunk(int rows, int V) {
+  const int pieces = (V + CHUNK - 1) / CHUNK;
+  const int64_t units = static_cast<int64_t>(rows) * pieces;
+  return units >= 4096 ? 4 : units >= 1024 ? 2 : 1;
+}
+
+static void launch_argmax(ArgParams& p, int dtype, int bs, int spc, hipStream_t st) {
+  p.n_chunks = ((p.V + CHUNK - 1) / CHUNK + spc - 1) / spc;
+  const dim3 grid(p.n_chunks, bs * p.W);
+  const bool bf = dtype == GSS_BF16;
+  switch (spc) {
+    case 4:
+      if (bf) hipLaunchKernelGGL((argmax_accept_kernel<uint16_t, 4>), grid, dim3(ARG_THREADS), 0, st, p);
+      else hipLaunchKernelGGL((argmax_accept_kernel<float, 4>), grid, dim3(ARG_THREADS), 0, st, p);
+      break;
+    case 2:
+      if (bf) hipLaunchKernelGGL((argmax_accept_kernel<uint16_t, 2>), grid, dim3(ARG_THREADS), 0, st, p);
+      else hipLaunchKernelGGL((argmax_accept_kernel<float, 2>), grid, dim3(ARG_THREADS), 0, st, p);
+      break;
+    default:
+      if (bf) hipLaunchKernelGGL((argmax_accept_kernel<uint16_t, 1>), grid, dim3(ARG_THREADS), 0, st, p);
+      else hipLaunchKernelGGL((argmax_accept_kernel<float, 1>), grid, dim3(ARG_THREADS), 0, st, p);
+  }
+}
+
 extern "C" int gss_argmax_workspace_size(int bs, int W, int V, size_t* bytes) {
   if (!bytes || bs <= 0 || W <= 0 || V <= 0) return GSS_ERR_ARG;
   if (W > MAX_W || V > MAX_CHUNKS * CHUNK) return GSS_ERR_UNSUPPORTED;
@@ -239,7 +294,6 @@ extern "C" int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, 
   p.W = W;
   p.V = V;
   p.flags = flags;
-  p.n_chunks = (V + CHUNK - 1) / CHUNK;
   p.window = window;
   p.target = target;
   p.accept_len = accept_len;
@@ -247,12 +301,7 @@ extern "C" int gss_argmax_accept(const void* logits, int dtype, int64_t ld_row, 
   p.packed = packed;
   p.counters = static_cast<uint32_t*>(workspace);
   p.part = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + PARTS_OFFSET);
-  const dim3 grid(p.n_chunks, bs * W);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == GSS_BF16)
-    hipLaunchKernelGGL(argmax_accept_kernel<uint16_t>, grid, dim3(ARG_THREADS), 0, st, p);
-  else
-    hipLaunchKernelGGL(argmax_accept_kernel<float>, grid, dim3(ARG_THREADS), 0, st, p);
+  launch_argmax(p, dtype, bs, pieces_per_chunk(bs * W, V), static_cast<hipStream_t>(stream));
   return gss_launch_status();
 }
 
@@ -322,7 +371,6 @@ extern "C" int gss_argmax_accept_noalloc(const void* logits, int dtype, int64_t 
   p.W = W;
   p.V = V;
   p.flags = flags;
-  p.n_chunks = (V + CHUNK - 1) / CHUNK;
   p.window = window;
   p.target = target;
   p.accept_len = accept_len;
@@ -330,11 +378,7 @@ extern "C" int gss_argmax_accept_noalloc(const void* logits, int dtype, int64_t 
   p.packed = packed;
   p.counters = static_cast<uint32_t*>(base);
   p.part = reinterpret_cast<uint64_t*>(static_cast<char*>(base) + NOALLOC_COUNTER_BYTES);
-  const dim3 grid(p.n_chunks, bs * W);
-  if (dtype == GSS_BF16)
-    hipLaunchKernelGGL(argmax_accept_kernel<uint16_t>, grid, dim3(ARG_THREADS), 0, st, p);
-  else
-    hipLaunchKernelGGL(argmax_accept_kernel<float>, grid, dim3(ARG_THREADS), 0, st, p);
+  launch_argmax(p, dtype, bs, pieces_per_chunk(bs * W, V), st);
   return gss_launch_status();
 }
 

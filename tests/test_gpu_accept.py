@@ -126,3 +126,23 @@ def test_workspace_shared_across_window_sizes(cuda):
             argmax_accept(logits.to(cuda), t, ws)
             torch.cuda.synchronize()
             np.testing.assert_array_equal(t.cpu().numpy(), tgt)
+
+
+@pytest.mark.parametrize("bs,V,dtype,ld_pad", [(32, 59393, torch.bfloat16, 24), (32, 12345, torch.float32, 0),
+                                               (8, 59392, torch.float32, 8), (1, 59392, torch.bfloat16, 0)],
+                         ids=["4-pieces-misaligned", "2-pieces-ragged", "2-pieces-f32", "1-piece"])
+def test_pieces_per_workgroup(cuda, bs, V, dtype, ld_pad):
+    """A workgroup scans 1, 2 or 4 pieces of 4096 logits depending on the batch's size (rows x pieces): every choice
+    gives the oracle's greedy ids, with ragged vocabularies (a partial last piece), misaligned rows (the scalar path),
+    planted NaNs and bf16 ties."""
+    print(f"pieces bs={bs} V={V} {dtype} pad={ld_pad}", flush=True)
+    W = 17
+    logits, window, _ = make_case(bs, W, V, seed=V + bs, dtype=dtype)
+    rows = logits.view(-1, V)
+    g = np.random.default_rng(V)
+    for r in g.choice(rows.shape[0], max(1, rows.shape[0] // 20), replace=False):
+        rows[r, int(g.integers(0, V))] = float("nan")  # NaN is the maximum; the lowest NaN index wins
+    tgt = argmax_first(logits.float().numpy())
+    t, acc, nx, packed = run(cuda, logits, window, ld_pad=ld_pad)
+    np.testing.assert_array_equal(t, tgt)
+    np.testing.assert_array_equal(acc, accept_chain(window, tgt))
