@@ -162,8 +162,8 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o, 64);
-    const int oi = __shfl_xor(bi, o, 64);
+    const float ov = lane_xor(bv, o);
+    const int oi = lane_xor(bi, o);
     if (beats(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
   __shared__ float sv[ARG_THREADS / 64];
@@ -441,9 +441,9 @@ __global__ void __launch_bounds__(ARG_THREADS) unmask_step_kernel(UnmaskParams p
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const float om = __shfl_xor(m, o, 64);
-    const int oi = __shfl_xor(mi, o, 64);
-    const float os = __shfl_xor(s, o, 64);
+    const float om = lane_xor(m, o);
+    const int oi = lane_xor(mi, o);
+    const float os = lane_xor(s, o);
     merge_softmax(m, mi, s, om, oi, os);
   }
   __shared__ float wm[ARG_THREADS / 64], ws[ARG_THREADS / 64];
@@ -515,8 +515,8 @@ __global__ void __launch_bounds__(ARG_THREADS) unmask_step_kernel(UnmaskParams p
     int bj = j < p.W ? j : 0x7fffffff;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
-      const float ob = __shfl_xor(best, o, 64);
-      const int oj = __shfl_xor(bj, o, 64);
+      const float ob = lane_xor(best, o);
+      const int oj = lane_xor(bj, o);
       if (beats(ob, oj, best, bj)) { best = ob; bj = oj; }
     }
     const bool un = masked && (c > p.threshold || j == bj);

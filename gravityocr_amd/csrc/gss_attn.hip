@@ -493,8 +493,8 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
           float mx = fmaxf(fmaxf(fmaxf(sacc[g][0][0], sacc[g][0][1]), fmaxf(sacc[g][0][2], sacc[g][0][3])),
                            fmaxf(fmaxf(sacc[g][1][0], sacc[g][1][1]), fmaxf(sacc[g][1][2], sacc[g][1][3])));
           if (__any(mx > m_run[g] + RESCALE_SLACK)) {  // wave-uniform: rescale O and l of the rows that moved
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = fmaxf(mx, lane_xor(mx, 16));
+            mx = fmaxf(mx, lane_xor(mx, 32));
             const float m_new = mx > m_run[g] + RESCALE_SLACK ? mx : m_run[g];
             // 1 for rows that keep their reference (also -inf: no visible key yet, where -inf - -inf would be NaN),
             // 0 on a row's first visible keys
@@ -531,8 +531,8 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
     // ---- the wave's rows: the row sums over the 4 lane groups, then O / l (bf16) and (m, l), or the output
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
-      l_run[g] += __shfl_xor(l_run[g], 16, 64);
-      l_run[g] += __shfl_xor(l_run[g], 32, 64);
+      l_run[g] += lane_xor(l_run[g], 16);
+      l_run[g] += lane_xor(l_run[g], 32);
       const int n = (nt0 + g) * 16 + l16;
       if (n >= p.R) continue;
       const float inv = l_run[g] > 0.f ? 1.f / l_run[g] : 0.f;
@@ -746,8 +746,8 @@ __global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams
     for (int g = 0; g < NG; ++g) {
       float mx = fmaxf(fmaxf(fmaxf(sacc[g][0][0], sacc[g][0][1]), fmaxf(sacc[g][0][2], sacc[g][0][3])),
                        fmaxf(fmaxf(sacc[g][1][0], sacc[g][1][1]), fmaxf(sacc[g][1][2], sacc[g][1][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = fmaxf(mx, lane_xor(mx, 16));
+      mx = fmaxf(mx, lane_xor(mx, 32));
       if (g4 == 0) smax[(wv * NG + g) * 16 + l16] = mx;
     }
     __syncthreads();
@@ -795,8 +795,8 @@ __global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams
   // its O (bf16) and l; then the waves share the (N-tile, 16-dim block) sums, each over the 8 waves in wave order.
 #pragma unroll
   for (int g = 0; g < NG; ++g) {
-    l_run[g] += __shfl_xor(l_run[g], 16, 64);
-    l_run[g] += __shfl_xor(l_run[g], 32, 64);
+    l_run[g] += lane_xor(l_run[g], 16);
+    l_run[g] += lane_xor(l_run[g], 32);
   }
   __syncthreads();  // every wave is done with the K/V stage: reuse it as scratch
   char* scr = reinterpret_cast<char*>(smem);
@@ -929,7 +929,7 @@ __global__ void __launch_bounds__(64) window_attn_merge(AttnParams p) {
 #pragma unroll
   for (int o = CPL; o < 64; o <<= 1)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+    for (int e = 0; e < 8; ++e) acc[e] += lane_xor(acc[e], o);
   if (sg != 0) return;
   const float inv = den > 0.f ? 1.f / den : 0.f;
   uint16_t* orow = p.out + ((static_cast<int64_t>(b) * p.W + n / p.G) * p.Hq + kvh * p.G + n % p.G) * D + dc * 8;

@@ -28,15 +28,49 @@ GSS_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, stat
 
 GSS_DEV float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// The value lane (lane ^ o) holds, for o in {1, 2, 4, 8, 16, 32}: what __shfl_xor(v, o, 64) returns, without its
+// LDS-crossbar round trip (~100 clocks each, six of them chained in a wave reduction): the gfx950 lane swaps across
+// 32 and across 16 lanes, and DPP within a row of 16 (rotating a row by 8 is xor 8; xor 4 takes the row shifted by
+// 4 one way or the other; xor 2 and 1 are quad permutations). Every lane of the wave must be active. With o a
+// constant after unrolling, the switch folds to one case.
+GSS_DEV uint32_t lane_xor(uint32_t u, int o) {
+  const int lane = threadIdx.x & 63;
+  switch (o) {
+    case 32: {
+      const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      return lane < 32 ? p[1] : p[0];
+    }
+    case 16: {
+      const auto p = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      return (lane & 16) ? p[0] : p[1];
+    }
+    case 8:
+      return __builtin_amdgcn_update_dpp(0u, u, 0x128, 0xf, 0xf, false);  // row_ror:8
+    case 4: {
+      const uint32_t r = __builtin_amdgcn_update_dpp(0u, u, 0x114, 0xf, 0xf, false);  // row_shr:4
+      const uint32_t l = __builtin_amdgcn_update_dpp(0u, u, 0x104, 0xf, 0xf, false);  // row_shl:4
+      return (lane & 4) ? r : l;
+    }
+    case 2:
+      return __builtin_amdgcn_update_dpp(0u, u, 0x4e, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    case 1:
+      return __builtin_amdgcn_update_dpp(0u, u, 0xb1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    default:
+      return static_cast<uint32_t>(__shfl_xor(static_cast<int>(u), o, 64));
+  }
+}
+GSS_DEV float lane_xor(float v, int o) { return __uint_as_float(lane_xor(__float_as_uint(v), o)); }
+GSS_DEV int lane_xor(int v, int o) { return static_cast<int>(lane_xor(static_cast<uint32_t>(v), o)); }
+
 GSS_DEV float wave_sum(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  for (int o = 32; o > 0; o >>= 1) v += lane_xor(v, o);
   return v;
 }
 
 GSS_DEV float wave_max(float v) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, lane_xor(v, o));
   return v;
 }
 

@@ -10,8 +10,8 @@ namespace {
 GSS_DEV int64_t wave_sum_i64(int64_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const int lo = __shfl_xor(static_cast<int>(v & 0xffffffff), o, 64);
-    const int hi = __shfl_xor(static_cast<int>(v >> 32), o, 64);
+    const int lo = lane_xor(static_cast<int>(v & 0xffffffff), o);
+    const int hi = lane_xor(static_cast<int>(v >> 32), o);
     v += (static_cast<int64_t>(hi) << 32) | static_cast<uint32_t>(lo);
   }
   return v;
