@@ -23,6 +23,8 @@ constexpr int PEN_PER_THREAD = 8;
 constexpr int MAX_K = 64;
 constexpr size_t COUNTER_STRIDE = 32;  // u32 per sequence counter (one 128-byte line each)
 constexpr int SV_MAX_WAVES = 16;
+constexpr uint32_t NARROW = 1u << 22;  // threshold search: full passes until [lo, hi] spans this many bit patterns
+constexpr int CAND_MAX = 512;          // then up to this many candidate tokens, searched by one wave
 
 enum { PEN_REPETITION = 1, PEN_PRESENCE = 2, PEN_FREQUENCY = 3, PEN_MIN_NEW_TOKENS = 4 };
 enum { FILTER_NONE = 0, FILTER_JOINT = 1, FILTER_TORCH = 2, FILTER_FI_MIN_P = 3 };
@@ -208,6 +210,9 @@ __global__ void __launch_bounds__(NTH) sample_rows_kernel(SvParams p) {
   __shared__ float2 red2[NW];
   __shared__ float scan[NTH];
   __shared__ float pd_s;
+  __shared__ float cand[CAND_MAX];  // threshold-search candidates
+  __shared__ int cnt_w[NW];
+  __shared__ uint32_t tau_s;
   const float* lr = p.logits + static_cast<int64_t>(row) * p.ld_row;
   const int v0 = tid * EPT;
   const float T = p.temperature[b];
@@ -268,12 +273,72 @@ __global__ void __launch_bounds__(NTH) sample_rows_kernel(SvParams p) {
       const int k = p.top_k[b] <= 0 ? 0x7fffffff : p.top_k[b];  // top_k <= 0: no top-k cut
       const float tp = p.top_p[b];
       // smallest tau (fp32 bit pattern in [lo, bits(PM)]) whose strictly-greater count C and mass MS pass the
-      // test; the tests are monotone in tau, so the kept tokens are exactly those with p >= tau
+      // test; the tests are monotone in tau, so the kept tokens are exactly those with p >= tau. Full passes over
+      // the row narrow [lo, hi] to at most NARROW bit patterns (~3% of a binade). Past that, tokens above hi count
+      // at every remaining tau (a constant count and mass, summed in the full passes' order) and tokens at or below
+      // lo never do, so the tokens in (lo, hi] are compacted into LDS in token order and wave 0 finishes the search
+      // over them alone (wave reductions, no workgroup barrier per step); more than CAND_MAX of them: full passes
+      // to the end. The candidate masses are added to the constant in a fixed order, so the test stays monotone and
+      // the result deterministic.
       const uint32_t top = __float_as_uint(PM);
       auto search = [&](uint32_t lo, auto&& ok) {
         uint32_t hi = top;
+        bool tried = false;  // the candidate compaction is attempted once
 #pragma unroll 1
         while (lo < hi) {
+          if (!tried && hi - lo <= NARROW) {
+            tried = true;
+            const float flo = __uint_as_float(lo), fhi = __uint_as_float(hi);
+            float c = 0.f, ms = 0.f;
+            int n = 0;
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) {
+              if (pr[e] > fhi) { c += 1.f; ms += pr[e]; }
+              n += pr[e] > flo && !(pr[e] > fhi) ? 1 : 0;
+            }
+            const float2 cm = block_sum2<NW>(c, ms, red2);  // also orders the LDS reuse below after earlier reads
+            // exclusive prefix of the candidate counts in thread order: within the wave, then the waves before it
+            int incl = n;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+              const int t = __shfl_up(incl, o, 64);
+              if ((tid & 63) >= o) incl += t;
+            }
+            if ((tid & 63) == 63) cnt_w[tid >> 6] = incl;
+            __syncthreads();
+            int off = incl - n, total = 0;
+            for (int w = 0; w < NW; ++w) {
+              const int t = cnt_w[w];
+              off += w < (tid >> 6) ? t : 0;
+              total += t;
+            }
+            if (total <= CAND_MAX) {  // workgroup-uniform
+#pragma unroll
+              for (int e = 0; e < EPT; ++e)
+                if (pr[e] > flo && !(pr[e] > fhi)) cand[off++] = pr[e];
+              __syncthreads();
+              if (tid < 64) {
+#pragma unroll 1
+                while (lo < hi) {
+                  const uint32_t mid = lo + (hi - lo) / 2;
+                  const float tau = __uint_as_float(mid);
+                  float cc = 0.f, mm = 0.f;
+                  for (int q = tid; q < total; q += 64) {  // lane order, then the wave sum
+                    const float x = cand[q];
+                    if (x > tau) { cc += 1.f; mm += x; }
+                  }
+                  cc = wave_sum(cc);
+                  mm = wave_sum(mm);
+                  if (ok(static_cast<int>(cm.x + cc), cm.y + mm)) hi = mid; else lo = mid + 1;
+                }
+                if (tid == 0) tau_s = lo;
+              }
+              __syncthreads();
+              lo = tau_s;
+              __syncthreads();  // every thread has read tau_s (a later search writes it again)
+              break;
+            }
+          }
           const uint32_t mid = lo + (hi - lo) / 2;
           const float tau = __uint_as_float(mid);
           float c = 0.f, ms = 0.f;
