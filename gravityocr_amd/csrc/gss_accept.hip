@@ -70,20 +70,6 @@ GSS_DEV int load16(const T* row, int j0, int V, float (&vals)[PER_THREAD]) {
   return n;
 }
 
-template <typename T>
-GSS_DEV void scan16(const T* row, int j0, int V, float& bv, int& bi) {
-  // 16 consecutive logits starting at j0 (in index order, so ties keep the earlier index)
-  float vals[PER_THREAD];
-  const int n = load16<T>(row, j0, V, vals);
-  if (n == PER_THREAD) {
-#pragma unroll
-    for (int e = 0; e < PER_THREAD; ++e)
-      if (beats(vals[e], j0 + e, bv, bi)) { bv = vals[e]; bi = j0 + e; }
-  } else {
-    for (int e = 0; e < n; ++e)
-      if (beats(vals[e], j0 + e, bv, bi)) { bv = vals[e]; bi = j0 + e; }
-  }
-}
 
 // Arrival counting of the (chunk, row) workgroups of one sequence, in two levels: workgroup g counts into sub-counter
 // g % SUB, the last arrival of each sub-counter counts into the sequence counter, and the last of those finishes the
@@ -135,29 +121,46 @@ __global__ void __launch_bounds__(ARG_THREADS) argmax_accept_kernel(ArgParams p)
 
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  if constexpr (SPC == 1) {
-    const int j0 = chunk * CHUNK + tid * PER_THREAD;
-    if (j0 < p.V) scan16<T>(lrow, j0, p.V, bv, bi);
-  } else {
-    float vals[SPC][PER_THREAD];
-    int n[SPC];
+  float vals[SPC][PER_THREAD];
+  int n[SPC];
+  bool full = true;
 #pragma unroll
-    for (int q = 0; q < SPC; ++q) {
-      const int j0 = (chunk * SPC + q) * CHUNK + tid * PER_THREAD;
-      n[q] = j0 < p.V ? load16<T>(lrow, j0, p.V, vals[q]) : 0;
+  for (int q = 0; q < SPC; ++q) {
+    const int j0 = (chunk * SPC + q) * CHUNK + tid * PER_THREAD;
+    if (j0 < p.V) {
+      n[q] = load16<T>(lrow, j0, p.V, vals[q]);
+    } else {
+      n[q] = 0;
+#pragma unroll
+      for (int e = 0; e < PER_THREAD; ++e) vals[q][e] = -INFINITY;
     }
+    full = full && n[q] == PER_THREAD;
+  }
+  // Fast path (every piece full, no NaN): the thread's maximum, then the lowest index holding it (ties between
+  // +0 and -0 compare equal, as in the rule). Otherwise the rule's own comparison, element by element.
+  float m = -INFINITY;
+  bool nan = false;
+#pragma unroll
+  for (int q = 0; q < SPC; ++q)
+#pragma unroll
+    for (int e = 0; e < PER_THREAD; ++e) {
+      nan = nan || vals[q][e] != vals[q][e];
+      m = fmaxf(m, vals[q][e]);
+    }
+  if (full && !nan) {
+    bv = m;
+#pragma unroll
+    for (int q = SPC - 1; q >= 0; --q)
+#pragma unroll
+      for (int e = PER_THREAD - 1; e >= 0; --e)
+        if (vals[q][e] == m) bi = (chunk * SPC + q) * CHUNK + tid * PER_THREAD + e;
+  } else {
 #pragma unroll
     for (int q = 0; q < SPC; ++q) {  // pieces in index order, each in index order
       const int j0 = (chunk * SPC + q) * CHUNK + tid * PER_THREAD;
-      if (n[q] == PER_THREAD) {
 #pragma unroll
-        for (int e = 0; e < PER_THREAD; ++e)
-          if (beats(vals[q][e], j0 + e, bv, bi)) { bv = vals[q][e]; bi = j0 + e; }
-      } else {
-#pragma unroll
-        for (int e = 0; e < PER_THREAD; ++e)
-          if (e < n[q] && beats(vals[q][e], j0 + e, bv, bi)) { bv = vals[q][e]; bi = j0 + e; }
-      }
+      for (int e = 0; e < PER_THREAD; ++e)
+        if (e < n[q] && beats(vals[q][e], j0 + e, bv, bi)) { bv = vals[q][e]; bi = j0 + e; }
     }
   }
 #pragma unroll
