@@ -181,3 +181,35 @@ def test_penalize_rows_without_min_new_tokens(cuda, order):
     penalize_rows(dl, torch.as_tensor(cand).to(cuda), dst, order)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(dl.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("kind", ["peaked-top-k", "flat-top-p", "all-equal", "equal-blocks"])
+def test_threshold_search_paths(cuda, kind):
+    """The threshold search finishes over compacted candidates when few tokens lie near the cut (a peaked row under
+    top-k 40; a flat row under top-p 0.95, after a second, narrower attempt) and by full passes when too many do (a
+    row of equal logits, where every token is a candidate at any width; blocks of exactly tied values straddling the
+    cut): every path draws from the oracle's distribution."""
+    from gravityocr_amd.kernels import sample_rows
+    print(f"threshold search {kind}", flush=True)
+    g = np.random.default_rng(len(kind))
+    bs, K, V = 2, 5, 59392
+    if kind == "peaked-top-k":
+        logits, T, k, tp = g.normal(size=(bs * K, V)) * 2.5, 0.8, 40, 0.9
+    elif kind == "flat-top-p":
+        logits, T, k, tp = g.normal(size=(bs * K, V)) * 0.5, 1.5, 0, 0.95
+    elif kind == "all-equal":
+        logits, T, k, tp = np.zeros((bs * K, V)), 1.0, 0, 0.9
+    else:
+        logits, T, k, tp = np.repeat(g.normal(size=(bs * K, V // 64)), 64, axis=1), 1.0, 0, 0.7
+    logits = logits.astype(np.float32)
+    u = g.uniform(0, 1, (bs, K)).astype(np.float32)
+    f = lambda x, dt: torch.tensor([x] * bs, dtype=dt, device=cuda)
+    sampled = torch.full((bs, K), -7, dtype=torch.int32, device=cuda)
+    sample_rows(torch.as_tensor(logits).to(cuda), bs, K, temperature=f(T, torch.float32), filter="joint",
+                top_k=f(k, torch.int32), top_p=f(tp, torch.float32), min_p=f(0.0, torch.float32),
+                uniforms=torch.as_tensor(u).to(cuda), sampled=sampled)
+    torch.cuda.synchronize()
+    got = sampled.cpu().numpy()
+    for r in range(bs * K):
+        q = S.target_probs(logits[r], T, 1, k if k > 0 else V + 1, tp)
+        assert _draw_ok(q, float(u.flat[r]), int(got.flat[r])), (r, int(got.flat[r]), S.inverse_cdf(q, float(u.flat[r])))
