@@ -7,8 +7,9 @@ kernel's exact operation sequence, so every row is computed the same way at ever
     gss_gemm_rope_stage             fused q|k|v projection, RoPE on q and k, window K/V staged (not yet in the cache)
     gss_draft_attn / gss_verify_attn   paged prefix + window, draft or verify mask, under the decoder's attention plan
     gss_gemm_parts (o_proj)         fp32 k-split partial sums
-    gss_add_rmsnorm_parts           residual + post-attention sandwich norm + the MLP input norm (optionally, at
-                                    <= 12 rows, the same norm inside the gate_up GEMM's prologue: fuse_gate_norm)
+    gss_add_rmsnorm_parts           residual + post-attention sandwich norm + the MLP input norm (at <= 12 rows
+                                    the same norm runs inside the gate_up GEMM's prologue instead: fuse_gate_norm,
+                                    on by default)
     gss_gemm_swiglu                 gate_up projection with the SwiGLU epilogue
     gss_gemm_parts (down)           fp32 k-split partial sums
     gss_add_rmsnorm_parts           residual + post-MLP norm + the next layer's input norm
@@ -70,9 +71,9 @@ class GssEngine:
         # the post-attention norms in the gate_up GEMM's prologue (persistent kernel: once per CU, while the first
         # weight tiles load) instead of a gss_add_rmsnorm launch; bit-identical to the separate norm, for at most 12
         # rows (one row per wave of the GEMM's 12) and a hidden size the prologue supports (a multiple of 512,
-        # <= 1536). Off: once gate_up's workgroups issue all their tiles' weights at once, the separate norm is
-        # faster for the 1-row AR step too (750 against 757 us per step on the 16-layer decoder)
-        self.fuse_gate_norm = False
+        # <= 1536). On: with the wave reductions on lane swaps and DPP the 1-row AR step takes 715 against 726 us
+        # on the 16-layer decoder (the windows of a round have more rows and keep the separate norm)
+        self.fuse_gate_norm = True
         self.gemm_parts = True    # o_proj / down as k-split partial sums (gemm_parts + the parts norms)
         self.device = torch.device(device)
         self.max_bs, self.max_len, self.max_win = max_bs, max_len, max_win

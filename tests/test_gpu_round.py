@@ -122,14 +122,15 @@ def test_spec_equals_ar_on_gpu(cuda, cfg_name, bd, n_tok):
 
 
 def test_gate_norm_prologue_equals_separate_norm(cuda):
-    """The optional gate_up-prologue norm (fuse_gate_norm, off by default) gives the AR steps' logits bit for bit."""
+    """The gate_up-prologue norm of the AR steps (fuse_gate_norm, on by default) gives the separate norm's logits bit
+    for bit."""
     from gravityocr_amd.model import GlmTextConfig
     cfg = GlmTextConfig(n_layers=4, hidden=1536, n_heads=16, n_kv_heads=2, head_dim=128, ffn=4608, vocab=59392)
     eng, dec, w, emb = build(cuda, cfg, 2, 500, 16, 16, 1024)
-    assert not eng.fuse_gate_norm
-    toks, logits = gpu_ar(eng, dec, emb, 12)
-    eng.fuse_gate_norm = True
+    assert eng.fuse_gate_norm
     toks_f, logits_f = gpu_ar(eng, dec, emb, 12)
+    eng.fuse_gate_norm = False
+    toks, logits = gpu_ar(eng, dec, emb, 12)
     assert toks_f == toks
     for a, b in zip(logits, logits_f):
         assert torch.equal(a, b)
