@@ -71,8 +71,10 @@ class GssEngine:
         # the post-attention norms in the gate_up GEMM's prologue (persistent kernel: once per CU, while the first
         # weight tiles load) instead of a gss_add_rmsnorm launch; bit-identical to the separate norm, for at most 12
         # rows (one row per wave of the GEMM's 12) and a hidden size the prologue supports (a multiple of 512,
-        # <= 1536). On: with the wave reductions on lane swaps and DPP the 1-row AR step takes 715 against 726 us
-        # on the 16-layer decoder (the windows of a round have more rows and keep the separate norm)
+        # <= 1536); with gemm_parts, the post-MLP norms likewise in the next layer's qkv prologue and the last one in
+        # the LM head's. On: with the wave reductions on lane swaps and DPP the 1-row AR step takes 715 against
+        # 726 us on the 16-layer decoder with the gate_up prologue alone (the windows of a round have more rows and
+        # keep the separate norms)
         self.fuse_gate_norm = True
         self.gemm_parts = True    # o_proj / down as k-split partial sums (gemm_parts + the parts norms)
         self.device = torch.device(device)
@@ -187,10 +189,23 @@ class GssEngine:
         c = self.cfg
         bs, W = b.bs, b.W
         ws = self.ws_gemm
-        h, h_alt = b.h, b.h2  # the residual stream; the gate_up prologue writes the updated one to the other buffer
+        h, h_alt = b.h, b.h2  # the residual stream; a GEMM prologue writes the updated one to the other buffer
+        # windows of at most 12 rows: every parts norm runs in the next GEMM's prologue (gate_up, the next layer's
+        # qkv, the LM head) instead of its own launch
+        fuse = (self.fuse_gate_norm and self.gemm_parts and (c.hidden // 64) % 4 == 0 and not self.post_norm
+                and bs * W <= 12 and c.hidden % 512 == 0 and c.hidden <= 1536)
+        pending = None  # down_proj's parts and the norm weights the next prologue applies to them
         for l in range(c.n_layers):
-            K.gemm_rope_stage(b.x, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l], rot_dim=c.rot_dim,
-                              pos_delta=pos_delta, workspace=ws)
+            if pending is not None:
+                K.gemm_rope_stage(None, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l],
+                                  rot_dim=c.rot_dim, pos_delta=pos_delta, workspace=ws,
+                                  pro=dict(a_parts=pending[0], h_in=h, h_out=h_alt, w_post=pending[1],
+                                           w_next=pending[2], eps=c.rms_eps))
+                h, h_alt = h_alt, h
+                pending = None
+            else:
+                K.gemm_rope_stage(b.x, self.wqkv[l], sl, self.inv_freq, b.q, b.k_win[l], b.v_win[l],
+                                  rot_dim=c.rot_dim, pos_delta=pos_delta, workspace=ws)
             K.window_attention(b.q, self.k_pages[l], self.v_pages[l], pt, sl, b.k_win[l], b.v_win[l], b.o,
                                n_causal=n_causal, scale=self.scale, plan=plan, workspace=self.ws_attn)
             nxt = self.n_in[l + 1] if l + 1 < c.n_layers else self.n_final
@@ -203,7 +218,7 @@ class GssEngine:
             elif self.gemm_parts and (c.hidden // 64) % 4 == 0:
                 # o_proj and down as k-split partial sums, added in split order by the norm that follows
                 K.gemm_parts(b.o.view(bs * W, -1), self.wo[l], b.ap_o)
-                if self.fuse_gate_norm and bs * W <= 12 and c.hidden % 512 == 0 and c.hidden <= 1536:
+                if fuse:
                     K.gemm_swiglu(None, self.wgu[l], b.act, workspace=ws,
                                   pro=dict(a_parts=b.ap_o, h_in=h, h_out=h_alt, w_post=self.n_psa[l],
                                            w_next=self.n_pa[l], eps=c.rms_eps))
@@ -212,7 +227,10 @@ class GssEngine:
                     K.add_rmsnorm_parts(b.ap_o, self.n_psa[l], h, self.n_pa[l], b.x, c.rms_eps)
                     K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
                 K.gemm_parts(b.act, self.wdown[l], b.ap_d)
-                K.add_rmsnorm_parts(b.ap_d, self.n_pm[l], h, nxt, b.x, c.rms_eps)
+                if fuse:
+                    pending = (b.ap_d, self.n_pm[l], nxt)
+                else:
+                    K.add_rmsnorm_parts(b.ap_d, self.n_pm[l], h, nxt, b.x, c.rms_eps)
             else:
                 K.gemm(b.o.view(bs * W, -1), self.wo[l], b.a, workspace=ws)
                 if self.fuse_gate_norm and bs * W <= 12 and c.hidden % 512 == 0 and c.hidden <= 1536:
@@ -225,12 +243,16 @@ class GssEngine:
                     K.gemm_swiglu(b.x, self.wgu[l], b.act, workspace=ws)
                 K.gemm(b.act, self.wdown[l], b.a, workspace=ws)
                 K.add_rmsnorm(b.a, self.n_pm[l], h, nxt, b.x, c.rms_eps)
+        x_in, pro = b.x, None
+        if pending is not None:  # the final norm in the LM head's prologue (the residual is not needed after it)
+            x_in, pro = None, dict(a_parts=pending[0], h_in=h, h_out=None, w_post=pending[1], w_next=pending[2],
+                                   eps=c.rms_eps)
         if getattr(b, "want_f32", False):
             if getattr(b, "logits32", None) is None:
                 b.logits32 = torch.empty(bs * W, c.vocab, dtype=torch.float32, device=self.device)
-            K.gemm(b.x, self.lm_head, b.logits32, workspace=ws)
+            K.gemm(x_in, self.lm_head, b.logits32, pro=pro, workspace=ws)
             return b.logits32.view(bs, W, c.vocab)
-        K.gemm(b.x, self.lm_head, b.logits, workspace=ws)
+        K.gemm(x_in, self.lm_head, b.logits, pro=pro, workspace=ws)
         return b.logits.view(bs, W, c.vocab)
 
     def _forward_fused(self, b: _Bufs, n_causal, sl, pt, pos_delta, plan) -> torch.Tensor:
