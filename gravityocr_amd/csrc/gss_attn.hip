@@ -870,17 +870,20 @@ __global__ void __launch_bounds__(64) window_attn_merge(AttnParams p) {
   // one round of loads: the length, and (m, l) and the first PRE * SGW partial rows of every split of the workspace
   // (in bounds whatever the length); the valid count masks them afterwards
   const int L = min(max(p.prefix_len[b] + p.prefix_extra, 0), p.cap);
+  // The loads are unconditional (splits past the workspace read split 0, which every row with keys has written), so
+  // no loaded value joins a branch: a register copy at such a join made the compiler wait for every load issued
+  // before it, splitting the round in two.
   float2 mlv[MLR];
 #pragma unroll
   for (int k = 0; k < MLR; ++k) {
     const int sp = lane + 64 * k;
-    mlv[k] = sp < ns ? ml[sp] : float2{-INFINITY, 0.f};
+    mlv[k] = ml[sp < ns ? sp : 0];
   }
   u32x4_t u[PRE];
 #pragma unroll
   for (int k = 0; k < PRE; ++k) {
     const int sp = sg + k * SGW;
-    u[k] = sp < ns ? *reinterpret_cast<const u32x4_t*>(obase + sp * ostride) : u32x4_t{0u, 0u, 0u, 0u};
+    u[k] = *reinterpret_cast<const u32x4_t*>(obase + (sp < ns ? sp : 0) * ostride);
   }
   const int nv = min(ns, valid_splits(L, p.W, p.tps));
   float mx = lane < nv ? mlv[0].x : -INFINITY;
