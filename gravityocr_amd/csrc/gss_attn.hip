@@ -579,6 +579,11 @@ __global__ void __launch_bounds__(RG_THREADS, 1) attn_rowgroup_kernel(AttnParams
   uint16_t* lds_k = smem;
   uint16_t* lds_v = smem + LdsRG<D>::V_OFF;
 
+  // The kernel arguments the exits and the first loads need, in one batch before the first branch: loaded where
+  // first used, they came in three dependent scalar round trips ahead of the prefix length's own.
+  asm volatile("" ::"s"(p.RG), "s"(p.n_units), "s"(p.n_split), "s"(p.Hkv), "s"(p.prefix_len), "s"(p.prefix_extra),
+               "s"(p.cap), "s"(p.tps), "s"(p.W), "s"(p.q), "s"(p.k_pages), "s"(p.v_pages), "s"(p.page_table),
+               "s"(p.pt_stride));
   // grid order: as attn_split_kernel (units spread over the XCDs, the row groups of a unit on one XCD)
   const int r8 = blockIdx.x % (8 * p.RG);
   const int u = blockIdx.x / (8 * p.RG) * 8 + r8 % 8, rg = r8 / 8;
