@@ -229,6 +229,11 @@ __global__ void __launch_bounds__(64 * RWT, 2) attn_split_kernel(AttnParams p) {
   // late splits are empty) thus spread their work evenly over the XCDs; numbering all units instead would put
   // split s of every sequence on XCD s % 8. Each workgroup finds its unit from the device-side lengths (wave 0 scans
   // the valid split counts of the batch), so the host needs no length and the launch stays graph-capturable.
+  // the kernel arguments of the exits, the unit scan and the first loads in one scalar batch before the first
+  // branch (loaded where first used, they came in dependent round trips)
+  asm volatile("" ::"s"(p.RG), "s"(p.n_units), "s"(p.bs), "s"(p.prefix_len), "s"(p.prefix_extra), "s"(p.cap),
+               "s"(p.n_split), "s"(p.W), "s"(p.tps), "s"(p.Hkv), "s"(p.q), "s"(p.k_pages), "s"(p.v_pages),
+               "s"(p.page_table), "s"(p.pt_stride), "s"(p.TPG), "s"(p.RW), "s"(p.R));
   const int r8 = blockIdx.x % (8 * p.RG);
   const int v = blockIdx.x / (8 * p.RG) * 8 + r8 % 8, rg = r8 / 8;
   if (v >= p.n_units) return;  // padding of the last group of 8 units

@@ -343,6 +343,11 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_kernel(GemmParams p, int ksw
   // LDS: [NW][FT][NT][64] wave partials, then (PRO_ADDNORM) x rows [M][Kd + XPAD] or (XS) per wave [M][ksw * 4]
   // 16-byte chunks of its k-range
   extern __shared__ floatx4_t red[];
+  // the kernel arguments of the staging, weight and RoPE loads in one scalar batch (loaded where first used, they
+  // came in two dependent round trips)
+  asm volatile("" ::"s"(p.x), "s"(p.ldx), "s"(p.w), "s"(p.ldw), "s"(p.M), "s"(p.N), "s"(p.Kd), "s"(p.kps),
+               "s"(p.seq_lens), "s"(p.pos_delta), "s"(p.inv_freq), "s"(p.rot_dim), "s"(p.W), "s"(p.D), "s"(ksw),
+               "s"(static_cast<int>(blockDim.x)));
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, NW = blockDim.x >> 6;
   const int l16 = lane & 15, g4 = lane >> 4;
   const int f0 = blockIdx.x * FT * 16;
