@@ -675,6 +675,11 @@ __global__ void __launch_bounds__(64 * MAX_NW) gemm_stream_kernel(GemmParams p, 
   auto tile_at = [&](int i) { return static_cast<int>(blockIdx.x) + i * G; };
   u32x4_t wa[UNR][FT], wb[UNR][FT], wc[UNR][FT];  // wc: the few-tile path's third tile
   uint16_t* xs = reinterpret_cast<uint16_t*>(red + red_sets * NW * FT * NT * 64);
+  // the arguments of the weight loads and of the prologue in one scalar batch (read where first used, the
+  // prologue's came in two more dependent round trips after the weight loads)
+  if constexpr (PRO == PRO_ADDNORM)
+    asm volatile("" ::"s"(p.w), "s"(p.ldw), "s"(p.N), "s"(p.Kd), "s"(p.M), "s"(p.h_in), "s"(p.w_next),
+                 "s"(p.pa_parts), "s"(p.n_parts), "s"(p.pa), "s"(p.w_post), "s"(p.eps), "s"(p.h_out));
   load_w(tile_at(0), wa);
   if constexpr (PRO == PRO_ADDNORM) {
     // the normalized rows, one wavefront per row, into LDS; workgroup 0 also stores the updated residual
